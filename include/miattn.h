@@ -1,0 +1,116 @@
+/*
+ * miattn.h -- C ABI of the MI355X (gfx950) attention hot path.
+ *
+ * Three operations, each a hand-written HIP kernel family in libmiattn.so:
+ *
+ *   mi_kv_slot_write   paged KV slot scatter   replaces PagedPool.write_slots
+ *                                              (reference model/paged.py:188-239, the two
+ *                                              index_copy_ calls at :238-239)
+ *   mi_paged_decode    block-table GQA decode  replaces paged_decode + _paged_decode_kernel
+ *                                              (reference model/triton_decode.py:250-328,
+ *                                              kernel :545-643)
+ *   mi_varlen_prefill  packed varlen causal    replaces FlashVarlen.prefill_varlen
+ *                      prefill attention       (reference model/attention/varlen.py:317-357)
+ *
+ * Conventions shared by every entry point:
+ *   - every pointer except the `host_*` arguments is a device pointer;
+ *   - strides are in ELEMENTS, not bytes;
+ *   - `stream` is a hipStream_t passed as void* (0 = the legacy default stream);
+ *   - the return value is MI_OK (0) or a negative MI_ERR_* code; mi_last_error() gives the
+ *     message of the last failing call on the calling host thread;
+ *   - no entry point allocates device memory: scratch space is a caller-owned workspace
+ *     whose size the matching *_workspace_size() query returns;
+ *   - launches are asynchronous on `stream`; nothing here synchronises the device.
+ */
+#ifndef MIATTN_H_
+#define MIATTN_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types of q/k/v/out and of the KV pools. */
+enum mi_dtype { MI_F32 = 0, MI_F16 = 1, MI_BF16 = 2 };
+
+/* Return codes. The Python shim maps INVALID/UNSUPPORTED/WORKSPACE to ValueError and
+ * LAUNCH to RuntimeError, the split the reference draws between caller bugs and
+ * environment failures (reference model/triton_decode.py:120-132). */
+enum mi_status {
+  MI_OK = 0,
+  MI_ERR_INVALID = -1,     /* argument/shape contract violated                         */
+  MI_ERR_UNSUPPORTED = -2, /* legal shape that no kernel instantiation covers           */
+  MI_ERR_WORKSPACE = -3,   /* workspace pointer/size does not cover the launch          */
+  MI_ERR_LAUNCH = -4       /* the HIP runtime rejected the launch                       */
+};
+
+/* Message of the last failing call on this host thread ("" when none). */
+const char* mi_last_error(void);
+
+/* ABI version: bumps whenever a signature below changes. */
+int mi_abi_version(void);
+
+/* ------------------------------------------------------------------ KV slot write
+ * Replaces PagedPool.write_slots (reference model/paged.py:188-239):
+ *     k_pool_flat[slot_ids[i]] = k[i];  v_pool_flat[slot_ids[i]] = v[i]
+ * over the flat (n_slots, H_kv, D) view of a (n_blocks, block_size, H_kv, D) pool.
+ * The pools are contiguous; k/v are (n_tokens, H_kv, D) with arbitrary element strides
+ * src_strides = {k_s0, k_s1, k_s2, v_s0, v_s1, v_s2}. slot_ids are int32
+ * (slot_bits == 32) or int64 (slot_bits == 64). A pure copy: bit-exact by construction.
+ * A slot outside [0, n_slots) is never written: the kernel skips that token and stores
+ * 1 + its index into *error_word (device int32, may be NULL) so the caller can raise
+ * without a per-call host synchronisation. Distinct slots are the caller's contract
+ * (reference model/paged.py:196-199); with duplicates the winner is unspecified. */
+int mi_kv_slot_write(const void* k, const void* v, const void* slot_ids, int slot_bits,
+                     void* k_pool, void* v_pool, int64_t n_tokens, int H_kv, int D,
+                     int64_t n_slots, const int64_t* src_strides, int dtype,
+                     int32_t* error_word, void* stream);
+
+/* ------------------------------------------------------------------ paged decode
+ * Replaces paged_decode (reference model/triton_decode.py:250-328) and its kernel
+ * (:545-643): one query token per row against a paged KV pool.
+ *   q            (B, H, D), strides {q_s0, q_s1, q_s2}, D contiguous (q_s2 == 1)
+ *   k/v_cache    (n_blocks, block_size, H_kv, D), D contiguous
+ *   block_table  (B, max_blocks) int32, row stride bt_s0, column-contiguous
+ *   seqlen       (B,) int32 in [0, max_blocks * block_size]
+ *   out          (B, H, D), strides {o_s0, o_s1, o_s2}
+ * strides = {q_s0,q_s1,q_s2, k_s0,k_s1,k_s2,k_s3, v_s0,v_s1,v_s2,v_s3, o_s0,o_s1,o_s2,
+ *            bt_s0}   (15 entries, elements)
+ * GQA: query head h reads KV head h / (H / H_kv). Softmax is fp32 online softmax in the
+ * log2 domain with scale*log2(e); out = acc / max(l, 1), so a zero-length row is exact
+ * zeros (reference :639). The page walk is clamped to max_blocks (reference :593) and
+ * block ids are trusted, as in the reference (:64-66). Long rows are split over
+ * workgroups (split-K) and merged by a log-sum-exp pass that uses the workspace. */
+size_t mi_paged_decode_workspace_size(int B, int H, int H_kv, int D, int block_size,
+                                      int max_blocks);
+int mi_paged_decode(const void* q, const void* k_cache, const void* v_cache,
+                    const int32_t* block_table, const int32_t* seqlen, void* out, int B,
+                    int H, int H_kv, int D, int block_size, int max_blocks,
+                    const int64_t* strides, float scale, int dtype, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------ varlen prefill
+ * Replaces FlashVarlen.prefill_varlen (reference model/attention/varlen.py:317-357):
+ * attention inside each cu_seqlens segment of a packed token axis, causal within the
+ * segment when `causal` is non-zero; q (total, H, D), k/v (total, H_kv, D), out
+ * (total, H, D), all contiguous; bf16 or fp16 (fp32 is MI_ERR_UNSUPPORTED, the same
+ * dtype contract as FA2, reference :338-343).
+ *   cu_seqlens      device int32 (n_seqs + 1)
+ *   tile_schedule   device int32 (n_tiles), built by mi_varlen_schedule
+ * The schedule orders query tiles heaviest-first so the causal triangle does not leave a
+ * tail of long tiles; it depends only on the segment lengths and H/H_kv, so a caller
+ * builds it once per packed group and reuses it for every layer. */
+int mi_varlen_schedule(const int32_t* host_cu_seqlens, int n_seqs, int H, int H_kv,
+                       int D, int causal, int32_t* host_schedule, int capacity);
+int mi_varlen_prefill(const void* q, const void* k, const void* v, void* out,
+                      const int32_t* cu_seqlens, int n_seqs, int total_tokens,
+                      int max_seqlen, const int32_t* tile_schedule, int n_tiles, int H,
+                      int H_kv, int D, float scale, int causal, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MIATTN_H_ */

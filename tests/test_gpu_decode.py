@@ -1,0 +1,268 @@
+"""Paged decode on the HIP kernel vs the CPU oracles (the reference's kernel tests,
+reference tests/unit/test_triton_decode.py:252-640, restated against this build).
+
+Tolerances: fp32 1e-4 and bf16/fp16 2e-2 max|delta| against the fp32 gather oracle
+(reference :288-292); the north-star bar of 1e-3 against an fp32 softmax is checked on
+the unrounded oracle with the output's own bf16 rounding allowance (2^-8 relative) added.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from miattn import PagedKV, PagedPool, paged_decode, paged_decode_plan
+from miattn import workloads as W
+from oracle.decode import dense_decode_f64, reference_paged_decode
+from oracle.seat import SeatSlab
+
+pytestmark = pytest.mark.gpu
+
+
+def _build(B, H, H_kv, D, bs, lengths, *, dtype=torch.float32, seed=0, n_blocks=None, device="cuda"):
+    gen = torch.Generator().manual_seed(seed)
+    pages = [(int(n) + bs - 1) // bs for n in lengths]
+    max_pages = max(max(pages), 1)
+    n_blocks = n_blocks or max(B * max_pages, max_pages + 4)
+    k = torch.randn(n_blocks, bs, H_kv, D, generator=gen).to(dtype)
+    v = torch.randn(n_blocks, bs, H_kv, D, generator=gen).to(dtype)
+    q = torch.randn(B, H, D, generator=gen).to(dtype)
+    table = torch.zeros(B, max_pages, dtype=torch.int32)
+    for row, n in enumerate(pages):
+        if n:
+            table[row, :n] = torch.randperm(n_blocks, generator=gen)[:n].to(torch.int32)
+    seqlen = torch.tensor(lengths, dtype=torch.int32)
+    return [t.to(device) for t in (q, k, v, table, seqlen)]
+
+
+def _cpu(*ts):
+    return [t.cpu() for t in ts]
+
+
+def _check_argmax(got, expected_f32):
+    """Argmax over D must agree wherever the oracle's top-2 gap exceeds bf16 rounding."""
+    top = expected_f32.topk(2, dim=-1).values
+    clear = (top[..., 0] - top[..., 1]) > 2e-2 * top[..., 0].abs().clamp(min=1)
+    assert torch.equal(got.float().argmax(-1)[clear], expected_f32.argmax(-1)[clear])
+
+
+SHAPES = [
+    pytest.param(1, 2, 2, 64, 16, [1], id="b1-gqa1-d64-l1-bs16"),
+    pytest.param(3, 8, 4, 128, 16, [15, 16, 17], id="b3-gqa2-d128-l15-17"),
+    pytest.param(8, 8, 2, 64, 32, [1, 15, 16, 17, 100, 1, 15, 16], id="b8-gqa4-d64-bs32"),
+    pytest.param(1, 8, 1, 256, 16, [1664], id="b1-gqa8-d256-l1664"),
+    pytest.param(3, 8, 1, 256, 32, [100, 1664, 1], id="b3-gqa8-d256-bs32"),
+    pytest.param(4, 16, 8, 128, 16, [2048, 700, 129, 5], id="qwen3-b4"),
+    pytest.param(2, 16, 8, 128, 16, [8192, 3001], id="qwen3-long-splitk"),
+    pytest.param(2, 8, 4, 32, 16, [77, 300], id="d32"),
+    pytest.param(2, 4, 2, 16, 16, [50, 33], id="d16"),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=["fp32", "bf16", "fp16"])
+@pytest.mark.parametrize("B,H,H_kv,D,bs,lengths", SHAPES)
+def test_paged_decode_matches_reference(B, H, H_kv, D, bs, lengths, dtype, cuda):
+    if D == 16 and dtype == torch.float32:
+        pytest.skip("fp32 D=16 is below the 16-byte lane slice; covered by bf16/fp16")
+    q, k, v, table, seqlen = _build(B, H, H_kv, D, bs, lengths, dtype=dtype, seed=13)
+    got = paged_decode(q, k, v, table, seqlen)
+    torch.cuda.synchronize()
+    assert got.shape == (B, H, D) and got.dtype == dtype
+    assert torch.isfinite(got).all()
+    expected = reference_paged_decode(*_cpu(q, k, v, table, seqlen), out_dtype=torch.float32)
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    diff = (got.cpu().float() - expected).abs().max().item()
+    assert diff < tol, f"max|delta| {diff} exceeded {tol}"
+    if dtype != torch.float32:
+        _check_argmax(got.cpu(), expected)
+        # <= 1e-3 against the fp32 softmax, beyond the output's rounding
+        excess = ((got.cpu().float() - expected).abs() - expected.abs() * 2.0 ** -8).max().item()
+        assert excess <= 1e-3, f"bf16 error beyond rounding {excess}"
+
+
+def test_small_case_against_the_float64_oracle(cuda):
+    q, k, v, table, seqlen = _build(2, 4, 2, 64, 16, [5, 17], seed=101)
+    got = paged_decode(q, k, v, table, seqlen)
+    expected = dense_decode_f64(*_cpu(q, k, v, table, seqlen))
+    torch.testing.assert_close(got.cpu(), expected, rtol=0, atol=1e-5)
+
+
+def test_kernel_masks_stale_bytes_in_a_reused_block(cuda):
+    bs, D, H, H_kv = 16, 64, 4, 2
+    gen = torch.Generator().manual_seed(107)
+    k = torch.empty(1, bs, H_kv, D)
+    v = torch.empty_like(k)
+    k[:, :5] = torch.randn(5, H_kv, D, generator=gen)
+    v[:, :5] = torch.randn(5, H_kv, D, generator=gen)
+    k[:, 5:] = 7.0
+    v[:, 5:] = -3.0
+    q = torch.randn(2, H, D, generator=gen)
+    table = torch.zeros(2, 1, dtype=torch.int32)
+    seqlen = torch.tensor([5, 15], dtype=torch.int32)
+    got = paged_decode(*[t.to(cuda) for t in (q, k, v, table, seqlen)])
+    expected = reference_paged_decode(q, k, v, table, seqlen)
+    torch.testing.assert_close(got.cpu(), expected, rtol=0, atol=1e-4)
+    assert not torch.equal(got[0], got[1])
+
+
+def test_int64_seqlen_and_non_contiguous_query(cuda):
+    q, k, v, table, seqlen = _build(2, 4, 2, 64, 16, [17, 15], seed=21)
+    q = q.transpose(1, 2).contiguous().transpose(1, 2)
+    assert not q.is_contiguous()
+    got = paged_decode(q, k, v, table, seqlen.to(torch.int64))
+    expected = reference_paged_decode(*_cpu(q.contiguous(), k, v, table, seqlen))
+    torch.testing.assert_close(got.cpu(), expected, rtol=0, atol=1e-4)
+
+
+def test_does_not_mutate_inputs(cuda):
+    q, k, v, table, seqlen = _build(3, 8, 4, 64, 16, [17, 15, 1], seed=17)
+    before = [t.clone() for t in (q, k, v, table, seqlen)]
+    paged_decode(q, k, v, table, seqlen)
+    for name, t, b in zip(("q", "k", "v", "table", "seqlen"), (q, k, v, table, seqlen), before):
+        assert torch.equal(t, b), f"paged_decode mutated {name}"
+
+
+def test_zero_length_rows_are_exact_zeros(cuda):
+    q, k, v, table, seqlen = _build(3, 4, 2, 64, 16, [0, 16, 17], seed=23)
+    out = paged_decode(q, k, v, table, seqlen)
+    assert torch.isfinite(out).all() and not out[0].any()
+    torch.testing.assert_close(out[1:].cpu(), reference_paged_decode(*_cpu(q, k, v, table, seqlen))[1:],
+                               rtol=0, atol=1e-4)
+
+
+def test_revalidates_after_an_in_place_seqlen_change(cuda):
+    q, k, v, table, seqlen = _build(2, 4, 2, 64, 16, [17, 15], seed=43)
+    paged_decode(q, k, v, table, seqlen)
+    seqlen[0] = 1
+    got = paged_decode(q, k, v, table, seqlen)
+    torch.testing.assert_close(got.cpu(), reference_paged_decode(*_cpu(q, k, v, table, seqlen)), rtol=0, atol=1e-4)
+    seqlen[1] = table.shape[1] * 16 + 1
+    with pytest.raises(ValueError, match="capacity"):
+        paged_decode(q, k, v, table, seqlen)
+
+
+def test_inference_tensors(cuda):
+    q, k, v, table, _ = _build(2, 4, 2, 64, 16, [17, 15], seed=47)
+    with torch.inference_mode():
+        seqlen = torch.tensor([17, 15], dtype=torch.int32, device=cuda)
+        got = paged_decode(q, k, v, table, seqlen)
+    torch.testing.assert_close(got.cpu(), reference_paged_decode(*_cpu(q, k, v, table, seqlen)), rtol=0, atol=1e-4)
+
+
+def test_error_surface(cuda):
+    q, k, v, table, seqlen = _build(2, 4, 2, 64, 16, [17, 15], seed=29)
+    with pytest.raises(ValueError, match="int32"):
+        paged_decode(q, k, v, table.long(), seqlen)
+    with pytest.raises(RuntimeError, match="CUDA tensors"):
+        paged_decode(q, k, v, table.cpu(), seqlen)
+    cap = table.shape[1] * k.shape[1]
+    with pytest.raises(ValueError, match="capacity"):
+        paged_decode(q, k, v, table, torch.full((2,), cap + 1, dtype=torch.int32, device=cuda))
+    with pytest.raises(ValueError, match="head_dim"):
+        paged_decode(q, k[..., :-1].contiguous(), v[..., :-1].contiguous(), table, seqlen)
+
+
+def test_plan_matches_paged_decode_for_every_layer(cuda):
+    q, k, v, table, seqlen = _build(3, 8, 4, 64, 16, [17, 15, 32], seed=43)
+    gen = torch.Generator(device=cuda).manual_seed(44)
+    ks = [torch.randn(k.shape, generator=gen, device=cuda) for _ in range(4)]
+    vs = [torch.randn(v.shape, generator=gen, device=cuda) for _ in range(4)]
+    plan = paged_decode_plan(q, ks, vs, table, seqlen)
+    for layer in range(4):
+        assert torch.equal(plan.run(layer, q), paged_decode(q, ks[layer], vs[layer], table, seqlen))
+
+
+def test_plan_contract_errors(cuda):
+    q, k, v, table, seqlen = _build(2, 4, 2, 64, 16, [17, 15], seed=59)
+    with pytest.raises(ValueError, match="int32 seqlen"):
+        paged_decode_plan(q, [k], [v], table, seqlen.to(torch.int64))
+    with pytest.raises(ValueError, match="column-contiguous block table"):
+        paged_decode_plan(q, [k], [v], table[:, ::2], seqlen)
+    with pytest.raises(ValueError, match="contiguous 1-D seqlen"):
+        paged_decode_plan(q, [k], [v], table, seqlen.repeat(2)[::2])
+    plan = paged_decode_plan(q, [k, k], [v, v], table, seqlen)
+    with pytest.raises(ValueError, match="does not match the validated layout"):
+        plan.run(0, q.transpose(1, 2).contiguous().transpose(1, 2))
+    with pytest.raises(ValueError, match="does not match the validated layout"):
+        plan.run(0, q.double())
+    with pytest.raises(IndexError, match="outside the plan"):
+        plan.run(2, q)
+
+
+def test_container_tracks_in_place_seqlen_updates(cuda):
+    """PagedKV's plan sees build_mask's in-place seqlen each step (reference :619-640)."""
+    pool = PagedPool(1, 4, 16, 2, 32, dtype=torch.float32, device=cuda, n_head=4)
+    kv = PagedKV(pool, [[0, 1, 2, 3]], [10], rope_len=64, n_head=4)
+    q = torch.randn(1, 4, 1, 32, device=cuda)
+    outs = []
+    for step in range(3):
+        kv.build_mask(next_token=True)
+        kv.write(0, torch.randn(1, 2, 1, 32, device=cuda), torch.randn(1, 2, 1, 32, device=cuda))
+        outs.append(kv.attend(0, q))
+        expected = paged_decode(q[:, :, 0].contiguous(), pool.keys[0], pool.values[0],
+                                kv._block_table_tensor, kv._seqlen).unsqueeze(2)
+        assert torch.equal(outs[-1], expected), f"step {step}"
+        kv.advance()
+    assert not torch.equal(outs[0], outs[-1])
+
+
+def test_config1_seat_shape_against_the_seat_path(cuda):
+    """Config 1 (B=8, 511 cached + 1, RoPE pre-applied): the paged kernel on the same
+    logical KV matches the CPU seat path within 2e-2 and the fp32 oracle within 1e-3."""
+    q, k, v = W.seat_decode_config1()
+    B, H_kv, L, D = k.shape
+    bs = 16
+    tables = W.block_tables_from_perm([L] * B, 512, bs, seed=7)
+    pool_k = torch.zeros(512, bs, H_kv, D, dtype=k.dtype)
+    pool_v = torch.zeros_like(pool_k)
+    for b, t in enumerate(tables):
+        for p, blk in enumerate(t):
+            pool_k[blk] = k[b, :, p * bs:(p + 1) * bs].permute(1, 0, 2)
+            pool_v[blk] = v[b, :, p * bs:(p + 1) * bs].permute(1, 0, 2)
+    table = torch.tensor(tables, dtype=torch.int32)
+    seqlen = torch.full((B,), L, dtype=torch.int32)
+    got = paged_decode(q[:, :, 0].to(cuda), pool_k.to(cuda), pool_v.to(cuda), table.to(cuda), seqlen.to(cuda)).cpu()
+    slab = SeatSlab(1, B, H_kv, D, L, dtype=k.dtype, n_head=q.shape[1])
+    slab.keys[0].copy_(k)
+    slab.values[0].copy_(v)
+    for b in range(B):
+        slab.activate(b, L)
+    slab.build_mask(next_token=False)
+    seat = slab.attend(0, q)[:, :, 0]
+    assert (got.float() - seat.float()).abs().max() <= 2e-2
+    f32 = reference_paged_decode(q[:, :, 0], pool_k, pool_v, table, seqlen, out_dtype=torch.float32)
+    excess = ((got.float() - f32).abs() - f32.abs() * 2.0 ** -8).max().item()
+    assert excess <= 1e-3
+
+
+def test_config2_one_layer_full_size(cuda):
+    """Config 2 at its real size (B=32, seqlen ~ U[128, 2048], 8192 blocks), one layer."""
+    inp = W.paged_decode_config(n_layer=1, device=cuda)
+    got = paged_decode(inp.q[0], inp.k_caches[0], inp.v_caches[0], inp.block_table, inp.seqlen).cpu()
+    expected = reference_paged_decode(inp.q[0].cpu(), inp.k_caches[0].cpu(), inp.v_caches[0].cpu(),
+                                      inp.block_table.cpu(), inp.seqlen.cpu(), out_dtype=torch.float32)
+    assert (got.float() - expected).abs().max() <= 2e-2
+    excess = ((got.float() - expected).abs() - expected.abs() * 2.0 ** -8).max().item()
+    assert excess <= 1e-3
+
+
+def test_config4_long_context_split_k(cuda):
+    """Config 4 rows (8192 tokens, permuted tables) vs the oracle, and block-permutation
+    invariance: moving every block to another physical slot (and the table with it)
+    leaves the output bitwise unchanged."""
+    inp = W.paged_decode_config(B=4, lengths=[8192] * 4, n_blocks=2048, n_layer=1, device=cuda, max_blocks=512)
+    got = paged_decode(inp.q[0], inp.k_caches[0], inp.v_caches[0], inp.block_table, inp.seqlen)
+    expected = reference_paged_decode(inp.q[0].cpu(), inp.k_caches[0].cpu(), inp.v_caches[0].cpu(),
+                                      inp.block_table.cpu(), inp.seqlen.cpu(), out_dtype=torch.float32)
+    assert (got.cpu().float() - expected).abs().max() <= 2e-2
+    perm = torch.randperm(2048, device=cuda)
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(2048, device=cuda)
+    k2 = torch.empty_like(inp.k_caches[0])
+    v2 = torch.empty_like(inp.v_caches[0])
+    k2[perm] = inp.k_caches[0]
+    v2[perm] = inp.v_caches[0]
+    table2 = perm[inp.block_table.long()].to(torch.int32)
+    assert torch.equal(paged_decode(inp.q[0], k2, v2, table2, inp.seqlen), got)
