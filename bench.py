@@ -70,6 +70,34 @@ class EventTimer:
         return self.start.elapsed_time(self.end)
 
 
+def time_graph(step, stream, steps: int, warmup: int):
+    """Capture ``step`` (a Python function that launches one step's kernels) into a HIP
+    graph on ``stream`` and time ``steps`` replays with events on that stream.
+
+    Returns (ms per step over the timed block, per-replay samples in ms)."""
+    with torch.cuda.stream(stream):
+        step()  # warm caches (schedules, workspaces) outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        step()
+    samples = []
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        with EventTimer(stream) as total:
+            for _ in range(steps):
+                graph.replay()
+        total_ms = total.ms()
+        for _ in range(min(steps, 50)):
+            with EventTimer(stream) as t:
+                graph.replay()
+            samples.append(t.ms())
+    torch.cuda.synchronize()
+    return total_ms / steps, samples
+
+
 def decode_bytes(lengths, B, H, H_kv, D, max_blocks, esize=2) -> int:
     kv = sum(lengths) * 2 * H_kv * D * esize
     qo = 2 * B * H * D * esize
@@ -77,7 +105,7 @@ def decode_bytes(lengths, B, H, H_kv, D, max_blocks, esize=2) -> int:
     return kv + qo + meta
 
 
-def bench_decode(inp, steps: int, warmup: int, stream):
+def bench_decode(inp, steps: int, warmup: int, stream, eager: bool = False):
     from miattn import paged_decode_plan
 
     B, H, D = inp.q[0].shape
@@ -90,35 +118,20 @@ def bench_decode(inp, steps: int, warmup: int, stream):
             outs[layer] = plan.run(layer, inp.q[layer])
 
     # eager step (Python launch path), for reference
-    for _ in range(3):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(10):
-        step()
-    torch.cuda.synchronize()
-    eager_ms = (time.perf_counter() - t0) * 1e3 / 10
-
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=stream):
-        step()
-    for _ in range(warmup):
-        graph.replay()
-    torch.cuda.synchronize()
-    per_step = []
     with torch.cuda.stream(stream):
+        for _ in range(3):
+            step()
         torch.cuda.synchronize()
-        with EventTimer(stream) as total:
-            for _ in range(steps):
-                graph.replay()
+        t0 = time.perf_counter()
+        for _ in range(10 if not eager else steps):
+            step()
         torch.cuda.synchronize()
-        # per-step samples for percentiles (separate pass, same graph)
-        for _ in range(min(steps, 50)):
-            with EventTimer(stream) as t:
-                graph.replay()
-            per_step.append(t.ms())
-    ms_per_step = total.ms() / steps
+    eager_ms = (time.perf_counter() - t0) * 1e3 / (10 if not eager else steps)
     nbytes = decode_bytes(inp.lengths, B, H, H_kv, D, inp.block_table.shape[1])
+    if eager:
+        ms_per_step, per_step = eager_ms, [eager_ms]
+    else:
+        ms_per_step, per_step = time_graph(step, stream, steps, warmup)
     return {
         "ms_per_step": ms_per_step,
         "eager_ms_per_step": eager_ms,
@@ -131,7 +144,9 @@ def bench_decode(inp, steps: int, warmup: int, stream):
     }
 
 
-def bench_prefill(stream, iters: int = 50):
+def bench_prefill(stream, steps: int = 20):
+    """Config 3: packed varlen prefill (28 layer calls on one packed group) and the packed
+    group's KV slot write (28 layers), each captured in a HIP graph and replayed."""
     from miattn import HipVarlen, PackedPrefill, PagedPool, PagedWriteSink
     from miattn import workloads as W
 
@@ -140,37 +155,37 @@ def bench_prefill(stream, iters: int = 50):
     H, D = inp.q.shape[1], inp.q.shape[2]
     flop = 4 * H * D * sum(n * (n + 1) // 2 for n in inp.lengths)  # causal pairs incl. diagonal
     ms = max(inp.lengths)
-    for _ in range(5):
-        backend.prefill_varlen(inp.q, inp.k, inp.v, cu_seqlens=inp.cu_seqlens, max_seqlen=ms)
-    torch.cuda.synchronize()
-    with EventTimer(stream) as t:
-        for _ in range(iters):
+
+    def prefill_step():
+        for _ in range(N_LAYER):
             backend.prefill_varlen(inp.q, inp.k, inp.v, cu_seqlens=inp.cu_seqlens, max_seqlen=ms)
-    prefill_ms = t.ms() / iters
+
+    prefill_step_ms, _ = time_graph(prefill_step, stream, steps, 3)
+    prefill_ms = prefill_step_ms / N_LAYER
     tflops = flop / (prefill_ms * 1e-3) / 1e12
 
     pool = PagedPool(N_LAYER, inp.n_blocks, inp.block_size, inp.k.shape[1], D, dtype=torch.bfloat16,
                      device="cuda", n_head=H)
     positions = torch.cat([torch.arange(n) for n in inp.lengths]).cuda()
-    k = inp.k.unsqueeze(0)
-    v = inp.v.unsqueeze(0)
-    write_times = []
-    for rep in range(6):
-        sinks = [PagedWriteSink(pool, t_, n) for t_, n in zip(inp.tables, inp.lengths)]
-        packed = PackedPrefill(cu_seqlens=inp.cu_seqlens, positions=positions, sinks=sinks, backend=backend)
-        torch.cuda.synchronize()
-        with EventTimer(stream) as t:
-            for layer in range(N_LAYER):
-                packed.write(layer, k, v)
-        if rep:
-            write_times.append(t.ms() / N_LAYER)
+    sinks = [PagedWriteSink(pool, t_, n) for t_, n in zip(inp.tables, inp.lengths)]
+    packed = PackedPrefill(cu_seqlens=inp.cu_seqlens, positions=positions, sinks=sinks, backend=backend)
+    slots = packed._packed_slots[1]
+    # distinct K/V sources per layer, so no layer's write reads what the previous one cached
+    ks = [torch.randn_like(inp.k) for _ in range(N_LAYER)]
+    vs = [torch.randn_like(inp.v) for _ in range(N_LAYER)]
+
+    def write_step():
+        for layer in range(N_LAYER):
+            pool.write_prefill_slots(layer, slots, ks[layer], vs[layer])
+
+    write_step_ms, _ = time_graph(write_step, stream, steps, 3)
     pool.check_writes()
-    write_ms = sum(write_times) / len(write_times)
+    write_ms = write_step_ms / N_LAYER
     write_bytes = 2 * 2 * sum(inp.lengths) * inp.k.shape[1] * D * 2 + sum(inp.lengths) * 8
     return {
         "workload": "config3: 8 prompts lognormal(median 512, sigma 0.6) clip [64,2048], H16/8 D128 bf16",
         "lengths": inp.lengths,
-        "prefill_ms_per_layer": prefill_ms,
+        "prefill_us_per_layer": prefill_ms * 1e3,
         "prefill_tflops": tflops,
         "prefill_frac_mfma_peak": tflops / BF16_MFMA_PEAK_TFLOPS,
         "prefill_tokens_per_s": sum(inp.lengths) / (prefill_ms * 1e-3),
@@ -178,7 +193,25 @@ def bench_prefill(stream, iters: int = 50):
         "slot_write_us_per_layer": write_ms * 1e3,
         "slot_write_gbs": write_bytes / (write_ms * 1e-3) / 1e9,
         "slot_write_frac_hbm_peak": write_bytes / (write_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "slot_write_bytes_per_layer": write_bytes,
     }
+
+
+def copy_calibration(mib: int, reps: int) -> dict:
+    """A plain device copy of a known size, run under the same PMC counters as the decode
+    kernel: FETCH_SIZE / WRITE_SIZE of this launch over its known bytes is the counters'
+    scale factor."""
+    n = mib * 2**20 // 2
+    src = torch.randn(n, device="cuda").to(torch.bfloat16)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / reps
+    return {"copy_mib": mib, "bytes_read": n * 2, "bytes_written": n * 2,
+            "gbs_read_plus_write": 2 * n * 2 / dt / 1e9}
 
 
 def bench_long_context(stream, steps: int = 10):
@@ -260,6 +293,10 @@ def main() -> int:
     ap.add_argument("--decode-only", action="store_true", help="only the headline decode leg (for profiling)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--eager", action="store_true", help="time the decode leg without graph capture "
+                    "(for counter collection, which needs plain kernel dispatches)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB (counter scale calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
@@ -274,11 +311,14 @@ def main() -> int:
     if not miattn.HIP_AVAILABLE:
         raise RuntimeError(f"libmiattn.so is not loadable: {miattn.LOAD_ERROR}")
     torch.cuda.set_device(0)
+    if args.copy_calibration:
+        print(json.dumps(copy_calibration(args.copy_calibration, 5)), flush=True)
+        return 0
     stream = torch.cuda.Stream()
     log("building config-2 inputs (28 layers, 8192 blocks each)")
     inp = W.paged_decode_config(device="cuda", max_blocks=128)
     log(f"decode: sum(seqlen)={inp.tokens}, B={len(inp.lengths)}")
-    dec = bench_decode(inp, args.steps, args.warmup, stream)
+    dec = bench_decode(inp, args.steps, args.warmup, stream, eager=args.eager)
     log(f"decode: {dec['us_per_layer']:.2f} us/layer, {dec['gbs']:.1f} GB/s")
     B, H, D = inp.q[0].shape
     H_kv = inp.k_caches[0].shape[2]
@@ -321,7 +361,8 @@ def main() -> int:
     if not args.decode_only:
         log("prefill + slot write (config 3)")
         line["prefill"] = bench_prefill(stream)
-        log(f"prefill: {line['prefill']['prefill_tflops']:.1f} TFLOP/s")
+        log(f"prefill: {line['prefill']['prefill_tflops']:.1f} TFLOP/s, "
+            f"slot write {line['prefill']['slot_write_gbs']:.1f} GB/s")
         log("long-context decode (config 4)")
         line["long_context"] = bench_long_context(stream)
         log(f"config4: {line['long_context']['gbs']:.1f} GB/s")

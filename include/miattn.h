@@ -81,10 +81,15 @@ int mi_kv_slot_write(const void* k, const void* v, const void* slot_ids, int slo
  * GQA: query head h reads KV head h / (H / H_kv). Softmax is fp32 online softmax in the
  * log2 domain with scale*log2(e); out = acc / max(l, 1), so a zero-length row is exact
  * zeros (reference :639). The page walk is clamped to max_blocks (reference :593) and
- * block ids are trusted, as in the reference (:64-66). Long rows are split over
- * workgroups (split-K) and merged by a log-sum-exp pass that uses the workspace. */
+ * block ids are trusted, as in the reference (:64-66).
+ *
+ * Split-K workspace: rows longer than one split are cut into splits whose (m, l, acc)
+ * partials go to the caller's workspace; a second launch on the same stream merges them
+ * (log-sum-exp) and writes `out`. mi_paged_decode_workspace_size() gives the exact size
+ * for a shape and dtype (0 when no row can need a split); the workspace must be 16-byte
+ * aligned. Calls that share one workspace must be ordered (one stream). */
 size_t mi_paged_decode_workspace_size(int B, int H, int H_kv, int D, int block_size,
-                                      int max_blocks);
+                                      int max_blocks, int dtype);
 int mi_paged_decode(const void* q, const void* k_cache, const void* v_cache,
                     const int32_t* block_table, const int32_t* seqlen, void* out, int B,
                     int H, int H_kv, int D, int block_size, int max_blocks,

@@ -5,20 +5,32 @@
 // with scale*log2(e), tail of the last page masked by `token < seqlen`, page walk clamped
 // to max_blocks, out = acc / max(l, 1) so an empty row is exact zeros.
 //
-// Different shape, chosen for MI355X:
-//   * one workgroup per (row, KV head, head chunk, split): the GB query heads that share a
-//     KV head are served by one workgroup, so each K/V byte is read from HBM once (the
+// Shape of the computation on MI355X:
+//   * one workgroup per (split, KV-head group). At the Qwen3 shape the group is all 8 KV
+//     heads, so a workgroup sweeps whole pages: one page of the (n_blocks, block_size,
+//     H_kv, D) pool is 16 tokens x 8 heads x 256 B = 32 KiB of contiguous K (and the same
+//     of V), read once from HBM in coalesced passes. Every query head of a KV head is
+//     served by the lanes holding that KV head, so each K/V byte is read once (the
 //     reference launches one program per query head and relies on the cache, :33-36);
-//   * split-K: a row's tokens are cut into `chunk`-token splits, one workgroup each, so
-//     B * H_kv = 256 units become thousands of workgroups and ragged rows balance over
-//     256 CUs; a log-sum-exp merge kernel folds the per-split (m, l, acc) partials;
-//   * lane layout: a KV row of one head (D elements) is spread over LPR = D*esize/16
-//     lanes holding 16 bytes each, so one wave-wide 16-byte load fetches 64/LPR whole
-//     token rows (4 rows of 256 B at D=128 bf16) straight into registers; the q.k dot is
-//     reduced across the LPR lanes with DPP butterflies, and each lane accumulates
-//     p * v for its own 16-byte slice of D;
-//   * each row of lanes keeps its own online-softmax state over the tokens it owns; the
-//     4 * RPW row states of a workgroup are merged through LDS at the end of the split.
+//   * token-balanced split-K, planned on the device: every workgroup reads the row lengths,
+//     sets chunk = ceil(sum(seqlen) / kTargetSplits) (rounded to a batch) and maps its
+//     index to (row, split) through a prefix sum of the rows' split counts. Every split
+//     therefore carries the same number of tokens however ragged the batch is, the grid
+//     (kTargetSplits + B workgroups, sized without a host read of seqlen) fills the 256
+//     CUs, and long rows (config 4) and short ones cost the same per token;
+//   * lane layout: a (token, KV head) row of D elements is spread over LPR = D*esize/16
+//     lanes holding 16 bytes each; a wave-wide 16-byte load covers 64/LPR rows and the
+//     four waves of a workgroup cover NR = 4*64/LPR rows = TPL consecutive tokens of the
+//     group's KVB heads. q.k is reduced over the LPR lanes with DPP/permlane butterflies;
+//     each lane accumulates p*v for its own 16-byte slice of D;
+//   * software pipeline: block-table entries are loaded two batches ahead and the K/V
+//     registers of the next batch are loaded while the current batch is reduced, so every
+//     wave keeps a batch of loads in flight;
+//   * a row that fits in one split is finished in place; otherwise each split writes its
+//     (m, l, acc) partial to the workspace and a second, small launch folds the partials
+//     with a log-sum-exp merge. (An in-kernel "last split merges" counter needs an
+//     agent-scope release per workgroup, which on the multi-XCD gfx950 writes back the
+//     XCD's L2 each time; measured several times slower than the extra launch.)
 // HBM-bound: per (token, KV head) the kernel reads 2 * D * esize bytes of K+V.
 #include "common.h"
 
@@ -26,66 +38,181 @@ namespace miattn {
 namespace {
 
 struct DecodeArgs {
-  int B, H, H_kv, G, n_hchunks, bs_log2, max_blocks, chunk, n_splits;
+  int B, H, H_kv, G, kvb_log2, n_hchunks, bs_log2, max_blocks, target, slots;
   int64_t qs0, qs1, ks0, ks1, ks2, vs0, vs1, vs2, os0, os1, bts0;
   float scale_log2;
 };
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-// Tokens per lane-row per batch: 2 * unroll 16-byte loads in flight per lane. Fewer when
-// one workgroup serves many query heads, whose scores and accumulators take the VGPRs.
-constexpr int unroll_for(int GB) { return GB <= 2 ? 8 : 16 / GB; }
+
+// Splits a launch aims for: 2 per CU of the 256-CU MI355X, all resident at once.
+#ifndef MIATTN_DECODE_TARGET_SPLITS
+#define MIATTN_DECODE_TARGET_SPLITS 512
+#endif
+constexpr int kTargetSplits = MIATTN_DECODE_TARGET_SPLITS;
+
+// Tokens per row state per batch, by query heads per lane: the next batch's K/V
+// registers (2 * U * 16 B per lane) are live while the current batch is reduced.
+#ifndef MIATTN_DECODE_UNROLL
+#define MIATTN_DECODE_UNROLL 4
+#endif
+constexpr int unroll_for(int GB) {
+  return GB <= 2 ? MIATTN_DECODE_UNROLL : (GB == 4 ? 4 : 2);
+}
 
 template <typename T, int D, int GB>
 struct Layout {
   static constexpr int esize = sizeof(T) == 4 ? 4 : 2;
-  static constexpr int EPL = 16 / esize;       // elements per lane
-  static constexpr int LPR = D / EPL;          // lanes per KV row
-  static constexpr int RPW = 64 / LPR;         // KV rows per wave-wide load
-  static constexpr int NR = kWaves * RPW;      // row states per workgroup
-  static constexpr int U = unroll_for(GB);     // tokens per row per batch
-  static constexpr int BATCH = NR * U;         // tokens per workgroup batch
+  static constexpr int EPL = 16 / esize;  // elements per lane
+  static constexpr int LPR = D / EPL;     // lanes per (token, KV head) row
+  static constexpr int RPW = 64 / LPR;    // rows per wave-wide load
+  static constexpr int NR = kWaves * RPW; // rows per workgroup-wide load
+  static constexpr int U = unroll_for(GB);
   static_assert(LPR >= 1 && LPR <= 64 && (64 % LPR) == 0, "unsupported D/dtype");
 };
 
+__device__ __forceinline__ int clamp_len(int len, int capacity) {
+  len = len < capacity ? len : capacity;  // page-walk clamp (reference :593)
+  return len > 0 ? len : 0;
+}
+
+// Tokens per split for a batch holding `total` tokens (identical in both launches).
+__device__ __forceinline__ int split_chunk(int total, int batch) {
+  int chunk = (total + kTargetSplits - 1) / kTargetSplits;
+  chunk = (chunk + batch - 1) / batch * batch;
+  return chunk > batch ? chunk : batch;
+}
+
+// Exclusive prefix sum over the workgroup; `total` receives the sum of all threads.
+__device__ __forceinline__ int block_exclusive_scan(int v, int* s_tmp, int& total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int inc = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int up = __shfl_up(inc, off, 64);
+    if (lane >= off) inc += up;
+  }
+  if (lane == 63) s_tmp[wave] = inc;
+  __syncthreads();
+  int before = 0;
+  total = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const int t = s_tmp[w];
+    before += w < wave ? t : 0;
+    total += t;
+  }
+  __syncthreads();
+  return before + inc - v;
+}
+
 template <typename T, int D, int GB>
-__global__ __launch_bounds__(kThreads) void decode_split_kernel(
+__global__ __launch_bounds__(kThreads) void paged_decode_kernel(
     const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc,
     const int32_t* __restrict__ block_table, const int32_t* __restrict__ seqlen,
-    T* __restrict__ out, float* __restrict__ ws_acc, float* __restrict__ ws_ml, DecodeArgs a) {
-  using L = Layout<T, D, GB>;
-  constexpr int EPL = L::EPL, LPR = L::LPR, RPW = L::RPW, NR = L::NR;
-  constexpr int kUnroll = L::U;
+    T* __restrict__ out, int32_t* __restrict__ ws_rows, float* __restrict__ ws_ml,
+    float* __restrict__ ws_acc, DecodeArgs a) {
+  using Lay = Layout<T, D, GB>;
+  constexpr int EPL = Lay::EPL, LPR = Lay::LPR, RPW = Lay::RPW, NR = Lay::NR, U = Lay::U;
   extern __shared__ float smem[];  // [NR][GB] m, [NR][GB] l, [NR][GB][D] acc
+  __shared__ int s_tmp[kWaves];
+  __shared__ int s_info[4];
 
-  const int split = blockIdx.x;
-  const int kvh = blockIdx.y / a.n_hchunks;
-  const int h0 = kvh * a.G + (blockIdx.y - kvh * a.n_hchunks) * GB;
-  const int b = blockIdx.z;
-
+  const int tid = threadIdx.x;
+  const int KVB = 1 << a.kvb_log2;
+  const int TPL = NR >> a.kvb_log2;  // tokens per workgroup-wide load
+  const int batch = TPL * U;
   const int capacity = a.max_blocks << a.bs_log2;
-  int len = seqlen[b];
-  len = len < capacity ? len : capacity;  // page-walk clamp (reference :593)
-  const int t_begin = split * a.chunk;
-  if (t_begin >= len) {
-    if (split == 0) {  // empty row: exact zeros, like acc / max(0, 1)
-      for (int i = threadIdx.x; i < GB * D; i += kThreads) {
-        const int g = i / D, d = i - g * D;
-        out[b * a.os0 + (h0 + g) * a.os1 + d] = from_f32<T>(0.0f);
-      }
-    }
-    return;
+
+  // ---- device-side split plan: total tokens -> chunk -> this workgroup's (row, split)
+  const int per = (a.B + kThreads - 1) / kThreads;  // rows per thread
+  const int rbeg = tid * per;
+  int lsum = 0;
+  for (int i = 0; i < per; ++i) {
+    const int row = rbeg + i;
+    if (row < a.B) lsum += clamp_len(seqlen[row], capacity);
   }
-  const int t_end = min(len, t_begin + a.chunk);
-  const int n_split_b = (len + a.chunk - 1) / a.chunk;
+  int total_tokens;
+  (void)block_exclusive_scan(lsum, s_tmp, total_tokens);
+  const int chunk = split_chunk(total_tokens, batch);
+  int nsum = 0;
+  for (int i = 0; i < per; ++i) {
+    const int row = rbeg + i;
+    if (row < a.B) nsum += (clamp_len(seqlen[row], capacity) + chunk - 1) / chunk;
+  }
+  int n_total;
+  const int excl = block_exclusive_scan(nsum, s_tmp, n_total);
+  const int w = blockIdx.x;
+  if (w >= n_total) return;  // uniform over the workgroup
+  if (w >= excl && w < excl + nsum) {  // exactly one thread owns w's row
+    int p = excl;
+    for (int i = 0; i < per; ++i) {
+      const int row = rbeg + i;
+      if (row >= a.B) break;
+      const int n_r = (clamp_len(seqlen[row], capacity) + chunk - 1) / chunk;
+      if (w < p + n_r) {
+        s_info[0] = row;
+        s_info[1] = w - p;
+        s_info[2] = n_r;
+        s_info[3] = p;
+        break;
+      }
+      p += n_r;
+    }
+  }
+  __syncthreads();
+  const int b = s_info[0], split = s_info[1], n_split_b = s_info[2], first_slot = s_info[3];
+  const int len = clamp_len(seqlen[b], capacity);
+  const int t_begin = split * chunk;
+  const int t_end = min(len, t_begin + chunk);
+  if (split == 0 && blockIdx.y == 0 && tid == 0) {
+    ws_rows[2 * b] = first_slot;  // read by the merge launch (always, so never stale)
+    ws_rows[2 * b + 1] = n_split_b;
+  }
 
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int r = lane / LPR;           // row within the wave
-  const int c = lane - r * LPR;       // 16-byte slice within the row
-  const int R = wave * RPW + r;       // row state index within the workgroup
+  const int grp = blockIdx.y / a.n_hchunks;  // KV-head group
+  const int hch = blockIdx.y - grp * a.n_hchunks;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int r = lane / LPR;          // row within the wave
+  const int c = lane - r * LPR;      // 16-byte slice of D within the row
+  const int R = wave * RPW + r;      // row state within the workgroup
+  const int kvl = R & (KVB - 1);     // KV head within the group
+  const int tsub = R >> a.kvb_log2;  // token within a workgroup-wide load
+  const int kvh = grp * KVB + kvl;
+  const int h0 = kvh * a.G + hch * GB;
 
+  const int32_t* bt_row = block_table + b * a.bts0;
+  const int bs_mask = (1 << a.bs_log2) - 1;
+  const T* kbase = kc + kvh * a.ks2 + c * EPL;
+  const T* vbase = vc + kvh * a.vs2 + c * EPL;
+
+  // Token u of a batch starting at t0; past t_end it falls back to t_begin (always valid)
+  // and is masked out of the softmax.
+  auto token = [&](int t0, int u) {
+    const int tok = t0 + u * TPL + tsub;
+    return tok < t_end ? tok : t_begin;
+  };
+  auto load_pages = [&](int t0, int (&pg)[U]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) pg[u] = bt_row[token(t0, u) >> a.bs_log2];
+  };
+  auto issue = [&](int t0, const int (&pg)[U], uint4 (&kr)[U], uint4 (&vr)[U]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int off = token(t0, u) & bs_mask;
+      kr[u] = load16(kbase + int64_t(pg[u]) * a.ks0 + off * a.ks1);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int off = token(t0, u) & bs_mask;
+      vr[u] = load16(vbase + int64_t(pg[u]) * a.vs0 + off * a.vs1);
+    }
+  };
+
+  int pg_next[U], pg_after[U];
+  load_pages(t_begin, pg_next);
   float qv[GB][EPL];
 #pragma unroll
   for (int g = 0; g < GB; ++g) {
@@ -103,69 +230,65 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(
     for (int e = 0; e < EPL; ++e) acc[g][e] = 0.0f;
   }
 
-  const int32_t* bt_row = block_table + b * a.bts0;
-  const int bs_mask = (1 << a.bs_log2) - 1;
-  const T* kbase = kc + kvh * a.ks2 + c * EPL;
-  const T* vbase = vc + kvh * a.vs2 + c * EPL;
-
-  for (int t0 = t_begin; t0 < t_end; t0 += L::BATCH) {
-    uint4 kr[kUnroll], vr[kUnroll];
-    bool valid[kUnroll];
+  uint4 kr[U], vr[U];
+  if (t_begin + batch < t_end) load_pages(t_begin + batch, pg_after);
+  issue(t_begin, pg_next, kr, vr);
+  for (int t0 = t_begin; t0 < t_end; t0 += batch) {
+    // issue order per iteration: pages two batches ahead, then K/V one batch ahead, so
+    // the in-order load counter never makes the K/V issue wait for this batch's data
+    uint4 kn[U], vn[U];
+    const bool more = t0 + batch < t_end;
+    if (more) {
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int tok = t0 + u * NR + R;
-      valid[u] = tok < t_end;
-      const int page = tok >> a.bs_log2;
-      const int64_t blk = valid[u] ? int64_t(bt_row[page]) : 0;
-      const int off = tok & bs_mask;
-      kr[u] = valid[u] ? load16(kbase + blk * a.ks0 + off * a.ks1) : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int tok = t0 + u * NR + R;
-      const int page = tok >> a.bs_log2;
-      const int64_t blk = valid[u] ? int64_t(bt_row[page]) : 0;
-      const int off = tok & bs_mask;
-      vr[u] = valid[u] ? load16(vbase + blk * a.vs0 + off * a.vs1) : make_uint4(0, 0, 0, 0);
+      for (int u = 0; u < U; ++u) pg_next[u] = pg_after[u];
+      if (t0 + 2 * batch < t_end) load_pages(t0 + 2 * batch, pg_after);
+      issue(t0 + batch, pg_next, kn, vn);
     }
 
-    float s[kUnroll][GB];
+    float s[U][GB];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
+      const bool valid = t0 + u * TPL + tsub < t_end;
 #pragma unroll
       for (int g = 0; g < GB; ++g) {
         float dot = 0.0f;
 #pragma unroll
         for (int e = 0; e < EPL; ++e) dot = fmaf(qv[g][e], Vec16<T>::get(kr[u], e), dot);
         dot = group_allreduce<LPR, SumOp>(dot);
-        s[u][g] = valid[u] ? dot * a.scale_log2 : -INFINITY;
+        s[u][g] = valid ? dot * a.scale_log2 : -INFINITY;
       }
     }
-
 #pragma unroll
     for (int g = 0; g < GB; ++g) {
       float mb = s[0][g];
 #pragma unroll
-      for (int u = 1; u < kUnroll; ++u) mb = fmaxf(mb, s[u][g]);
+      for (int u = 1; u < U; ++u) mb = fmaxf(mb, s[u][g]);
       const float m_new = fmaxf(m[g], mb);
       const float m_use = m_new == -INFINITY ? 0.0f : m_new;
       const float alpha = fast_exp2(m[g] - m_use);
       m[g] = m_new;
-      float lsum = l[g] * alpha;
+      float lsum_g = l[g] * alpha;
 #pragma unroll
       for (int e = 0; e < EPL; ++e) acc[g][e] *= alpha;
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
+      for (int u = 0; u < U; ++u) {
         const float p = fast_exp2(s[u][g] - m_use);
-        lsum += p;
+        lsum_g += p;
 #pragma unroll
         for (int e = 0; e < EPL; ++e) acc[g][e] = fmaf(p, Vec16<T>::get(vr[u], e), acc[g][e]);
       }
-      l[g] = lsum;
+      l[g] = lsum_g;
+    }
+    if (more) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        kr[u] = kn[u];
+        vr[u] = vn[u];
+      }
     }
   }
 
-  // Merge the NR row states of this workgroup through LDS.
+  // Merge the TPL row states of each KV head through LDS.
   float* sm_m = smem;
   float* sm_l = sm_m + NR * GB;
   float* sm_acc = sm_l + NR * GB;
@@ -180,57 +303,89 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(
   }
   __syncthreads();
 
-  for (int i = threadIdx.x; i < GB * D; i += kThreads) {
-    const int g = i / D, d = i - g * D;
+  const int n_out = KVB * GB * D;
+  const int64_t slot = first_slot + split;
+  for (int i = tid; i < n_out; i += kThreads) {
+    const int kl = i / (GB * D), g = (i / D) % GB, d = i % D;
     float M = -INFINITY;
-    for (int j = 0; j < NR; ++j) M = fmaxf(M, sm_m[j * GB + g]);
+    for (int ts = 0; ts < TPL; ++ts) M = fmaxf(M, sm_m[((ts << a.kvb_log2) + kl) * GB + g]);
     const float M_use = M == -INFINITY ? 0.0f : M;
     float Ls = 0.0f, As = 0.0f;
-    for (int j = 0; j < NR; ++j) {
-      const float w = fast_exp2(sm_m[j * GB + g] - M_use);
-      Ls = fmaf(sm_l[j * GB + g], w, Ls);
-      As = fmaf(sm_acc[(j * GB + g) * D + d], w, As);
+    for (int ts = 0; ts < TPL; ++ts) {
+      const int Rs = (ts << a.kvb_log2) + kl;
+      const float wgt = fast_exp2(sm_m[Rs * GB + g] - M_use);
+      Ls = fmaf(sm_l[Rs * GB + g], wgt, Ls);
+      As = fmaf(sm_acc[(Rs * GB + g) * D + d], wgt, As);
     }
-    const int h = h0 + g;
+    const int h = (grp * KVB + kl) * a.G + hch * GB + g;
     if (n_split_b <= 1) {
       out[b * a.os0 + h * a.os1 + d] = from_f32<T>(As / fmaxf(Ls, 1.0f));
     } else {
-      const int64_t slot = (int64_t(b) * a.H + h) * a.n_splits + split;
-      ws_acc[slot * D + d] = As;
+      const int64_t ph = slot * a.H + h;
+      ws_acc[ph * D + d] = As;
       if (d == 0) {
-        ws_ml[slot * 2 + 0] = M;
-        ws_ml[slot * 2 + 1] = Ls;
+        ws_ml[ph * 2 + 0] = M;
+        ws_ml[ph * 2 + 1] = Ls;
       }
     }
   }
 }
 
-// Log-sum-exp merge of the split partials of one (row, query head); rows that fit in one
-// split were finished by the split kernel and are skipped here.
+// Second launch, one workgroup per (query head, row): zero-length rows get exact zeros;
+// rows split over several workgroups get the log-sum-exp merge of their partials (the
+// (m, l) pairs are read in parallel, so the only serial part is the weighted sum over
+// splits); single-split rows were finished by the first launch.
 template <typename T, int D>
-__global__ __launch_bounds__(D) void decode_merge_kernel(const int32_t* __restrict__ seqlen,
-                                                         const float* __restrict__ ws_acc,
-                                                         const float* __restrict__ ws_ml,
-                                                         T* __restrict__ out, DecodeArgs a) {
+__global__ __launch_bounds__(256) void paged_decode_merge_kernel(
+    const int32_t* __restrict__ seqlen, const int32_t* __restrict__ ws_rows,
+    const float* __restrict__ ws_ml, const float* __restrict__ ws_acc, T* __restrict__ out,
+    DecodeArgs a) {
+  extern __shared__ float sw[];  // [n] weights
+  __shared__ float s_red[4];
   const int h = blockIdx.x;
   const int b = blockIdx.y;
+  const int tid = threadIdx.x;
   const int capacity = a.max_blocks << a.bs_log2;
-  int len = seqlen[b];
-  len = len < capacity ? len : capacity;
-  const int n = (len + a.chunk - 1) / a.chunk;
-  if (n <= 1) return;
-  const int d = threadIdx.x;
-  const int64_t base = (int64_t(b) * a.H + h) * a.n_splits;
-  float M = -INFINITY;
-  for (int s = 0; s < n; ++s) M = fmaxf(M, ws_ml[(base + s) * 2]);
-  const float M_use = M == -INFINITY ? 0.0f : M;
-  float Ls = 0.0f, As = 0.0f;
-  for (int s = 0; s < n; ++s) {
-    const float w = fast_exp2(ws_ml[(base + s) * 2] - M_use);
-    Ls = fmaf(ws_ml[(base + s) * 2 + 1], w, Ls);
-    As = fmaf(ws_acc[(base + s) * D + d], w, As);
+  const int len = clamp_len(seqlen[b], capacity);
+  T* orow = out + b * a.os0 + h * a.os1;
+  if (len == 0) {
+    for (int d = tid; d < D; d += blockDim.x) orow[d] = from_f32<T>(0.0f);
+    return;
   }
-  out[b * a.os0 + h * a.os1 + d] = from_f32<T>(As / fmaxf(Ls, 1.0f));
+  // Split 0 of every non-empty row recorded where the row's partials start and how many
+  // there are; a row the first launch finished in place (one split) needs nothing here.
+  const int first = ws_rows[2 * b];
+  const int n_split = ws_rows[2 * b + 1];
+  if (n_split <= 1) return;
+  const int64_t base = int64_t(first) * a.H + h;
+  float mloc = -INFINITY;
+  for (int s = tid; s < n_split; s += blockDim.x) mloc = fmaxf(mloc, ws_ml[(base + int64_t(s) * a.H) * 2]);
+  mloc = group_allreduce<64, MaxOp>(mloc);
+  if ((tid & 63) == 0) s_red[tid >> 6] = mloc;
+  __syncthreads();
+  float M = s_red[0];
+  for (int wv = 1; wv < int(blockDim.x >> 6); ++wv) M = fmaxf(M, s_red[wv]);
+  const float M_use = M == -INFINITY ? 0.0f : M;
+  float lloc = 0.0f;
+  for (int s = tid; s < n_split; s += blockDim.x) {
+    const int64_t ph = base + int64_t(s) * a.H;
+    const float wgt = fast_exp2(ws_ml[ph * 2] - M_use);
+    sw[s] = wgt;
+    lloc = fmaf(ws_ml[ph * 2 + 1], wgt, lloc);
+  }
+  lloc = group_allreduce<64, SumOp>(lloc);
+  __syncthreads();
+  if ((tid & 63) == 0) s_red[tid >> 6] = lloc;
+  __syncthreads();
+  float Ls = 0.0f;
+  for (int wv = 0; wv < int(blockDim.x >> 6); ++wv) Ls += s_red[wv];
+  const float inv = 1.0f / fmaxf(Ls, 1.0f);
+  for (int d = tid; d < D; d += blockDim.x) {
+    float As = 0.0f;
+#pragma unroll 8
+    for (int s = 0; s < n_split; ++s) As = fmaf(ws_acc[(base + int64_t(s) * a.H) * D + d], sw[s], As);
+    orow[d] = from_f32<T>(As * inv);
+  }
 }
 
 int ilog2_exact(int x) {
@@ -243,80 +398,92 @@ bool supported_d(int D) { return D == 16 || D == 32 || D == 64 || D == 128 || D 
 
 int esize_of(int dtype) { return dtype == MI_F32 ? 4 : (dtype == MI_F16 || dtype == MI_BF16) ? 2 : 0; }
 
-template <typename T, int D, int GB>
-size_t smem_bytes() {
-  return size_t(Layout<T, D, GB>::NR) * GB * (D + 2) * sizeof(float);
-}
+int lowbit(int x) { return x & -x; }
 
-// Heads per workgroup: the largest of 8/4/2/1 that divides the GQA group and keeps the
-// LDS merge buffer within 64 KiB.
-int pick_gb(int G, int NR, int D) {
-  for (int gb = 8; gb >= 1; gb /= 2) {
-    if (G % gb == 0 && size_t(NR) * gb * (D + 2) * 4 <= 65536) return gb;
-  }
-  return 1;
-}
+// Launch geometry, computed identically by the workspace query and the launcher.
+struct Plan {
+  int GB, n_hchunks, KVB, kvb_log2, n_groups, NR, TPL, U, slots;
+  size_t rows_bytes, ml_bytes, acc_bytes;
+  size_t smem_bytes;
+};
 
-int rows_per_batch(int dtype, int D, int GB) {
+Plan make_plan(int B, int H, int H_kv, int D, int dtype) {
+  Plan p{};
   const int es = esize_of(dtype);
   const int lpr = D * es / 16;
-  return kWaves * (64 / lpr) * unroll_for(GB);
-}
-
-// Tokens per split: as large as 256 (fewer partials to merge) but small enough that the
-// grid has >= 2048 workgroups to spread over 256 CUs, never below one batch.
-int pick_chunk(int B, int H_kv, int n_hchunks, int capacity, int batch) {
-  int chunk = batch > 256 ? batch : 256;
-  while (chunk > batch && chunk > 64) {
-    const long long wgs = (long long)B * H_kv * n_hchunks * ((capacity + chunk - 1) / chunk);
-    if (wgs >= 2048) break;
-    chunk /= 2;
+  p.NR = kWaves * (64 / lpr);
+  const int G = H / H_kv;
+  // Query heads per lane: the largest of 8/4/2/1 dividing G whose LDS merge buffer fits
+  // in 64 KiB.
+  p.GB = 1;
+  for (int gb = 8; gb >= 1; gb /= 2) {
+    if (G % gb == 0 && size_t(p.NR) * gb * (D + 2) * 4 <= 65536) {
+      p.GB = gb;
+      break;
+    }
   }
-  return chunk;
+  p.n_hchunks = G / p.GB;
+  p.KVB = lowbit(H_kv) < p.NR ? lowbit(H_kv) : p.NR;
+  p.kvb_log2 = ilog2_exact(p.KVB);
+  p.n_groups = H_kv / p.KVB;
+  p.TPL = p.NR / p.KVB;
+  p.U = unroll_for(p.GB);
+  // Splits never exceed kTargetSplits + B: chunk >= total / kTargetSplits, and each row
+  // adds at most one partial split.
+  p.slots = kTargetSplits + B;
+  p.smem_bytes = size_t(p.NR) * p.GB * (D + 2) * sizeof(float);
+  p.rows_bytes = (size_t(B) * 2 * sizeof(int32_t) + 255) / 256 * 256;
+  p.ml_bytes = size_t(p.slots) * H * 2 * sizeof(float);
+  p.acc_bytes = size_t(p.slots) * H * D * sizeof(float);
+  return p;
 }
 
 template <typename T, int D, int GB>
 int launch_typed(const void* q, const void* kc, const void* vc, const int32_t* bt,
-                 const int32_t* seqlen, void* out, float* ws_acc, float* ws_ml,
-                 const DecodeArgs& a, hipStream_t stream) {
-  const size_t smem = smem_bytes<T, D, GB>();
-  dim3 grid(a.n_splits, a.H_kv * a.n_hchunks, a.B);
-  hipLaunchKernelGGL((decode_split_kernel<T, D, GB>), grid, dim3(kThreads), smem, stream,
+                 const int32_t* seqlen, void* out, int32_t* ws_rows, float* ws_ml,
+                 float* ws_acc, const DecodeArgs& a, const Plan& p, hipStream_t stream) {
+  if (Layout<T, D, GB>::U != p.U || Layout<T, D, GB>::NR != p.NR) {
+    return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode: internal launch-geometry mismatch");
+  }
+  dim3 grid(p.slots, p.n_groups * p.n_hchunks);
+  hipLaunchKernelGGL((paged_decode_kernel<T, D, GB>), grid, dim3(kThreads), p.smem_bytes, stream,
                      static_cast<const T*>(q), static_cast<const T*>(kc),
-                     static_cast<const T*>(vc), bt, seqlen, static_cast<T*>(out), ws_acc, ws_ml,
-                     a);
+                     static_cast<const T*>(vc), bt, seqlen, static_cast<T*>(out), ws_rows, ws_ml,
+                     ws_acc, a);
   int rc = launch_status("mi_paged_decode (split kernel)");
-  if (rc != MI_OK || a.n_splits <= 1) return rc;
-  hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3(a.H, a.B), dim3(D), 0, stream, seqlen,
-                     ws_acc, ws_ml, static_cast<T*>(out), a);
+  if (rc != MI_OK) return rc;
+  const int threads = D > 64 ? D : 64;
+  hipLaunchKernelGGL((paged_decode_merge_kernel<T, D>), dim3(a.H, a.B), dim3(threads),
+                     size_t(p.slots) * sizeof(float), stream, seqlen, ws_rows, ws_ml, ws_acc,
+                     static_cast<T*>(out), a);
   return launch_status("mi_paged_decode (merge kernel)");
 }
 
 template <typename T, int D>
-int dispatch_gb(int GB, const void* q, const void* kc, const void* vc, const int32_t* bt,
-                const int32_t* seqlen, void* out, float* ws_acc, float* ws_ml,
-                const DecodeArgs& a, hipStream_t s) {
-  switch (GB) {
-    case 1: return launch_typed<T, D, 1>(q, kc, vc, bt, seqlen, out, ws_acc, ws_ml, a, s);
-    case 2: return launch_typed<T, D, 2>(q, kc, vc, bt, seqlen, out, ws_acc, ws_ml, a, s);
-    case 4: return launch_typed<T, D, 4>(q, kc, vc, bt, seqlen, out, ws_acc, ws_ml, a, s);
-    case 8: return launch_typed<T, D, 8>(q, kc, vc, bt, seqlen, out, ws_acc, ws_ml, a, s);
+int dispatch_gb(const void* q, const void* kc, const void* vc, const int32_t* bt,
+                const int32_t* seqlen, void* out, int32_t* ws_rows, float* ws_ml, float* ws_acc,
+                const DecodeArgs& a, const Plan& p, hipStream_t s) {
+  switch (p.GB) {
+    case 1: return launch_typed<T, D, 1>(q, kc, vc, bt, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, s);
+    case 2: return launch_typed<T, D, 2>(q, kc, vc, bt, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, s);
+    case 4: return launch_typed<T, D, 4>(q, kc, vc, bt, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, s);
+    case 8: return launch_typed<T, D, 8>(q, kc, vc, bt, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, s);
   }
-  return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode: no kernel for %d heads per workgroup", GB);
+  return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode: no kernel for %d heads per lane", p.GB);
 }
 
 template <typename T>
-int dispatch_d(int D, int GB, const void* q, const void* kc, const void* vc, const int32_t* bt,
-               const int32_t* seqlen, void* out, float* ws_acc, float* ws_ml,
-               const DecodeArgs& a, hipStream_t s) {
+int dispatch_d(int D, const void* q, const void* kc, const void* vc, const int32_t* bt,
+               const int32_t* seqlen, void* out, int32_t* ws_rows, float* ws_ml, float* ws_acc,
+               const DecodeArgs& a, const Plan& p, hipStream_t s) {
   switch (D) {
     case 16:
-      if constexpr (sizeof(T) == 2) return dispatch_gb<T, 16>(GB, q, kc, vc, bt, seqlen, out, ws_acc, ws_ml, a, s);
+      if constexpr (sizeof(T) == 2) return dispatch_gb<T, 16>(q, kc, vc, bt, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, s);
       break;
-    case 32: return dispatch_gb<T, 32>(GB, q, kc, vc, bt, seqlen, out, ws_acc, ws_ml, a, s);
-    case 64: return dispatch_gb<T, 64>(GB, q, kc, vc, bt, seqlen, out, ws_acc, ws_ml, a, s);
-    case 128: return dispatch_gb<T, 128>(GB, q, kc, vc, bt, seqlen, out, ws_acc, ws_ml, a, s);
-    case 256: return dispatch_gb<T, 256>(GB, q, kc, vc, bt, seqlen, out, ws_acc, ws_ml, a, s);
+    case 32: return dispatch_gb<T, 32>(q, kc, vc, bt, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, s);
+    case 64: return dispatch_gb<T, 64>(q, kc, vc, bt, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, s);
+    case 128: return dispatch_gb<T, 128>(q, kc, vc, bt, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, s);
+    case 256: return dispatch_gb<T, 256>(q, kc, vc, bt, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, s);
   }
   return fail(MI_ERR_UNSUPPORTED,
               "mi_paged_decode: head_dim %d is not supported by the HIP decode kernel "
@@ -324,23 +491,20 @@ int dispatch_d(int D, int GB, const void* q, const void* kc, const void* vc, con
               D);
 }
 
-size_t workspace_bytes_for(int B, int H, int D, int n_splits) {
-  if (n_splits <= 1) return 0;
-  return size_t(B) * H * n_splits * (size_t(D) + 2) * sizeof(float);
+bool shape_ok(int B, int H, int H_kv, int D, int block_size, int max_blocks, int dtype) {
+  return B > 0 && H > 0 && H_kv > 0 && H % H_kv == 0 && ilog2_exact(block_size) >= 0 &&
+         max_blocks > 0 && esize_of(dtype) != 0 && supported_d(D) && !(D == 16 && dtype == MI_F32);
 }
 
 }  // namespace
 }  // namespace miattn
 
 extern "C" size_t mi_paged_decode_workspace_size(int B, int H, int H_kv, int D, int block_size,
-                                                 int max_blocks) {
-  (void)H_kv;
-  if (B <= 0 || H <= 0 || D <= 0 || block_size <= 0 || max_blocks <= 0) return 0;
-  // Upper bound over every dtype and chunk choice: the smallest chunk the launcher picks
-  // is 64 tokens.
-  const long long capacity = (long long)max_blocks * block_size;
-  const int n_splits = int((capacity + 63) / 64);
-  return miattn::workspace_bytes_for(B, H, D, n_splits);
+                                                 int max_blocks, int dtype) {
+  using namespace miattn;
+  if (!shape_ok(B, H, H_kv, D, block_size, max_blocks, dtype)) return 0;
+  const Plan p = make_plan(B, H, H_kv, D, dtype);
+  return p.rows_bytes + p.ml_bytes + p.acc_bytes;
 }
 
 extern "C" int mi_paged_decode(const void* q, const void* k_cache, const void* v_cache,
@@ -368,6 +532,10 @@ extern "C" int mi_paged_decode(const void* q, const void* k_cache, const void* v
   }
   if (strides == nullptr) return fail(MI_ERR_INVALID, "mi_paged_decode: strides is NULL");
   if (B == 0) return MI_OK;
+  if ((long long)max_blocks * block_size * B > 2147483647LL) {
+    return fail(MI_ERR_UNSUPPORTED,
+                "mi_paged_decode: B * max_blocks * block_size must stay below 2^31 tokens");
+  }
   const int64_t* st = strides;
   // 16-byte vector access needs a contiguous head_dim and 16-byte aligned rows.
   const int es = esize_of(dtype);
@@ -384,29 +552,26 @@ extern "C" int mi_paged_decode(const void* q, const void* k_cache, const void* v
                 (long long)st[0], (long long)st[1], (long long)st[2], (long long)st[3],
                 (long long)st[4], (long long)st[5], (long long)st[6]);
   }
-  const int G = H / H_kv;
-  const int lpr = D * es / 16;
-  const int NR = kWaves * (64 / lpr);
-  const int GB = pick_gb(G, NR, D);
-  const int n_hchunks = G / GB;
-  const int capacity = max_blocks * block_size;
-  const int batch = rows_per_batch(dtype, D, GB);
-  const int chunk = pick_chunk(B, H_kv, n_hchunks, capacity, batch);
-  const int n_splits = (capacity + chunk - 1) / chunk;
-  if (n_splits > 65535 || H_kv * n_hchunks > 65535 || B > 65535) {
-    return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode: grid too large (B=%d, splits=%d)", B, n_splits);
+  const Plan p = make_plan(B, H, H_kv, D, dtype);
+  if (p.n_groups * p.n_hchunks > 65535 || B > 65535 || H > 65535) {
+    return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode: grid too large (B=%d, H=%d)", B, H);
   }
-  const size_t need = workspace_bytes_for(B, H, D, n_splits);
-  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
+  const size_t need = p.rows_bytes + p.ml_bytes + p.acc_bytes;
+  if (workspace == nullptr || workspace_bytes < need) {
     return fail(MI_ERR_WORKSPACE, "mi_paged_decode: workspace of %zu bytes < %zu needed",
                 workspace_bytes, need);
   }
-  float* ws_acc = static_cast<float*>(workspace);
-  float* ws_ml = need > 0 ? ws_acc + size_t(B) * H * n_splits * D : nullptr;
+  if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0) {
+    return fail(MI_ERR_WORKSPACE, "mi_paged_decode: workspace must be 16-byte aligned");
+  }
+  int32_t* ws_rows = static_cast<int32_t*>(workspace);
+  float* ws_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + p.rows_bytes);
+  float* ws_acc = ws_ml + p.ml_bytes / sizeof(float);
 
   DecodeArgs a;
-  a.B = B; a.H = H; a.H_kv = H_kv; a.G = G; a.n_hchunks = n_hchunks; a.bs_log2 = bs_log2;
-  a.max_blocks = max_blocks; a.chunk = chunk; a.n_splits = n_splits;
+  a.B = B; a.H = H; a.H_kv = H_kv; a.G = H / H_kv; a.kvb_log2 = p.kvb_log2;
+  a.n_hchunks = p.n_hchunks; a.bs_log2 = bs_log2;
+  a.max_blocks = max_blocks; a.target = kTargetSplits; a.slots = p.slots;
   a.qs0 = st[0]; a.qs1 = st[1];
   a.ks0 = st[3]; a.ks1 = st[4]; a.ks2 = st[5];
   a.vs0 = st[7]; a.vs1 = st[8]; a.vs2 = st[9];
@@ -416,9 +581,9 @@ extern "C" int mi_paged_decode(const void* q, const void* k_cache, const void* v
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
-    case MI_F32: return dispatch_d<float>(D, GB, q, k_cache, v_cache, block_table, seqlen, out, ws_acc, ws_ml, a, s);
-    case MI_F16: return dispatch_d<f16_t>(D, GB, q, k_cache, v_cache, block_table, seqlen, out, ws_acc, ws_ml, a, s);
-    case MI_BF16: return dispatch_d<bf16_t>(D, GB, q, k_cache, v_cache, block_table, seqlen, out, ws_acc, ws_ml, a, s);
+    case MI_F32: return dispatch_d<float>(D, q, k_cache, v_cache, block_table, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, s);
+    case MI_F16: return dispatch_d<f16_t>(D, q, k_cache, v_cache, block_table, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, s);
+    case MI_BF16: return dispatch_d<bf16_t>(D, q, k_cache, v_cache, block_table, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, s);
   }
   return fail(MI_ERR_INVALID, "mi_paged_decode: unknown dtype %d", dtype);
 }

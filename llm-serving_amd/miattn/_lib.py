@@ -58,7 +58,7 @@ SIGNATURES: dict[str, tuple] = {
         [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p, _c_int64, _c_int,
          _c_int, _c_int64, _p_int64, _c_int, _c_void_p, _c_void_p],
     ),
-    "mi_paged_decode_workspace_size": (_c_size_t, [_c_int] * 6),
+    "mi_paged_decode_workspace_size": (_c_size_t, [_c_int] * 7),
     "mi_paged_decode": (
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int,
@@ -75,7 +75,7 @@ SIGNATURES: dict[str, tuple] = {
     ),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 def _load():

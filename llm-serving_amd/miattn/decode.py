@@ -20,10 +20,12 @@ Contract (unchanged from the reference): ``q`` ``(B, H, D)``; ``k_cache``/``v_ca
 with values in ``[0, max_blocks * block_size]``; ``scale=None`` means ``1/sqrt(D)``.
 
 What differs underneath: the kernel is ``mi_paged_decode`` in ``libmiattn.so`` (one
-workgroup per (row, KV head, split) serving all GQA query heads, split-K with a
-log-sum-exp merge). Split-K needs a workspace; ``paged_decode`` takes it from torch's
-caching allocator per call and a plan owns one for all its layers, so the runs of one plan
-must stay ordered on one stream (the decode layer loop is). The kernels also need the K/V
+workgroup per (row, split, KV-head group) sweeping whole pages for every KV head and
+serving all GQA query heads; rows longer than one split are merged by a small
+log-sum-exp launch). Split-K needs a workspace;
+``paged_decode`` takes one from torch's caching allocator per call and a plan owns one for
+all its layers, so the runs of one plan must stay ordered on one stream (the decode layer
+loop is). The kernels also need the K/V
 pools' ``head_dim`` to be contiguous and 16-byte aligned, which every pool
 ``PagedPool`` allocates is; any other layout raises ``ValueError``.
 """
@@ -157,7 +159,9 @@ def _validate(q, k_cache, v_cache, block_table, seqlen) -> None:
 
 
 def _workspace(q, H: int, H_kv: int, D: int, block_size: int, max_blocks: int) -> torch.Tensor | None:
-    n = int(_lib.lib.mi_paged_decode_workspace_size(q.shape[0], H, H_kv, D, block_size, max_blocks))
+    """Split-K partials buffer, sized exactly for this shape and dtype (None if unneeded)."""
+    n = int(_lib.lib.mi_paged_decode_workspace_size(q.shape[0], H, H_kv, D, block_size, max_blocks,
+                                                     _lib.dtype_code(q.dtype)))
     if n == 0:
         return None
     return torch.empty(n, dtype=torch.uint8, device=q.device)
