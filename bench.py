@@ -144,7 +144,7 @@ def bench_decode(inp, steps: int, warmup: int, stream, eager: bool = False):
     }
 
 
-def bench_prefill(stream, steps: int = 20):
+def bench_prefill(stream, steps: int = 20, eager: bool = False):
     """Config 3: packed varlen prefill (28 layer calls on one packed group) and the packed
     group's KV slot write (28 layers), each captured in a HIP graph and replayed."""
     from miattn import HipVarlen, PackedPrefill, PagedPool, PagedWriteSink
@@ -160,7 +160,16 @@ def bench_prefill(stream, steps: int = 20):
         for _ in range(N_LAYER):
             backend.prefill_varlen(inp.q, inp.k, inp.v, cu_seqlens=inp.cu_seqlens, max_seqlen=ms)
 
-    prefill_step_ms, _ = time_graph(prefill_step, stream, steps, 3)
+    if eager:  # plain dispatches, for counter collection
+        with torch.cuda.stream(stream):
+            for _ in range(2):
+                prefill_step()
+            torch.cuda.synchronize()
+            with EventTimer(stream) as t:
+                prefill_step()
+            prefill_step_ms = t.ms()
+    else:
+        prefill_step_ms, _ = time_graph(prefill_step, stream, steps, 3)
     prefill_ms = prefill_step_ms / N_LAYER
     tflops = flop / (prefill_ms * 1e-3) / 1e12
 
@@ -178,7 +187,15 @@ def bench_prefill(stream, steps: int = 20):
         for layer in range(N_LAYER):
             pool.write_prefill_slots(layer, slots, ks[layer], vs[layer])
 
-    write_step_ms, _ = time_graph(write_step, stream, steps, 3)
+    if eager:
+        with torch.cuda.stream(stream):
+            write_step()
+            torch.cuda.synchronize()
+            with EventTimer(stream) as t:
+                write_step()
+            write_step_ms = t.ms()
+    else:
+        write_step_ms, _ = time_graph(write_step, stream, steps, 3)
     pool.check_writes()
     write_ms = write_step_ms / N_LAYER
     write_bytes = 2 * 2 * sum(inp.lengths) * inp.k.shape[1] * D * 2 + sum(inp.lengths) * 8
@@ -291,6 +308,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--decode-only", action="store_true", help="only the headline decode leg (for profiling)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the config-3 prefill and slot-write legs (for profiling)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--eager", action="store_true", help="time the decode leg without graph capture "
@@ -315,6 +334,9 @@ def main() -> int:
         print(json.dumps(copy_calibration(args.copy_calibration, 5)), flush=True)
         return 0
     stream = torch.cuda.Stream()
+    if args.prefill_only:
+        print(json.dumps({"prefill": bench_prefill(stream, args.steps, eager=args.eager)}), flush=True)
+        return 0
     log("building config-2 inputs (28 layers, 8192 blocks each)")
     inp = W.paged_decode_config(device="cuda", max_blocks=128)
     log(f"decode: sum(seqlen)={inp.tokens}, B={len(inp.lengths)}")

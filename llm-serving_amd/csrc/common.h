@@ -31,12 +31,10 @@ __device__ __forceinline__ float to_f32(f16_t x) {
 
 template <typename T> __device__ __forceinline__ T from_f32(float x);
 template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
-// Round-to-nearest-even, NaN kept quiet: the same rounding torch uses for .to(bfloat16).
+// Round-to-nearest-even (v_cvt_pk_bf16_f32 on gfx950), NaN kept quiet: the same rounding
+// torch uses for .to(bfloat16).
 template <> __device__ __forceinline__ bf16_t from_f32<bf16_t>(float x) {
-  uint32_t u = __float_as_uint(x);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return bf16_t{uint16_t((u >> 16) | 0x40)};
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return bf16_t{uint16_t(u >> 16)};
+  return bf16_t{__builtin_bit_cast(uint16_t, (__bf16)x)};
 }
 template <> __device__ __forceinline__ f16_t from_f32<f16_t>(float x) {
   return f16_t{__half_as_ushort(__float2half_rn(x))};

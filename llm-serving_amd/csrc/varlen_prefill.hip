@@ -6,21 +6,27 @@
 // scores. FlashAttention-2 style: one pass over K/V tiles with an fp32 online softmax.
 //
 // MI355X shape of the computation:
-//   * a workgroup (4 waves) owns one query tile of one packed segment for HPW query heads
-//     that share a KV head; every wave owns 32 query rows of one head, so the K/V tile
-//     staged in LDS is shared by all 4 waves (and by both GQA heads at Qwen3's 16/8);
+//   * a workgroup (4 waves) owns 64 query rows of one head of one packed segment. Wave w
+//     takes query block w & 1 (32 rows) and key half w >> 1 of every 64-key tile, so the
+//     serial chain of the longest causal tile is half its keys; the two key halves of a
+//     query block are folded at the end through LDS (log-sum-exp merge);
+//   * K and V tiles are double-buffered in LDS: the next tile's global loads are issued
+//     before the current tile's MFMAs and land in registers, which are written to the
+//     other buffer afterwards, so one barrier per tile remains. K is stored row-major; V
+//     is stored transposed (V^T[d][key]) through a 4x8 register transpose and 8-byte LDS
+//     writes, which is the operand layout the PV product needs;
 //   * scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16 (A = K from
 //     LDS, B = Q held in VGPRs for the whole loop). In the 32x32 accumulator layout each
 //     lane then owns one query column, so the row max needs one cross-lane exchange
 //     (lane ^ 32) and the row sum none until the end;
 //   * O^T = V^T P^T with the same MFMA: P^T comes straight from the score registers
-//     (packed to bf16), and V is stored transposed in LDS while it is staged, so the A
-//     operand is two 8-byte LDS reads per lane; the key order inside a 16-key MFMA step
-//     is permuted identically on both operands to match the score accumulator layout;
-//   * causal tiles above the diagonal are never visited; the diagonal tile is masked;
-//   * the grid is (head group, schedule entry): head groups are the fastest-varying
-//     index, so with 8 head groups every tile of one KV head lands on the same XCD and
-//     its K/V stay in that XCD's L2; schedule entries are ordered heaviest-first.
+//     (packed to bf16), the A operand is two 8-byte LDS reads per lane, and the key order
+//     inside a 16-key MFMA step is permuted identically on both operands to match the
+//     score accumulator layout;
+//   * causal tiles above the diagonal are never loaded; the diagonal tile is masked;
+//   * grid = (head, schedule entry), entries ordered heaviest-first; heads are permuted so
+//     the query heads of one KV head are dispatched to the same XCD and its K/V tiles are
+//     served from that XCD's L2.
 #include <algorithm>
 #include <type_traits>
 #include <vector>
@@ -35,6 +41,16 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
 
 constexpr int kThreads = 256;
+constexpr int kBQ = 64;  // query rows per workgroup
+constexpr int kBK = 64;  // keys per tile (two halves of 32)
+constexpr int kXcds = 8; // MI355X: 8 XCDs, workgroups dispatched round-robin over them
+
+// K/V tiles in flight in registers while a tile is computed: 1 (tile it+1) or 2 (it+1 and
+// it+2; twice the staging registers).
+#ifndef MIATTN_PREFILL_DEPTH
+#define MIATTN_PREFILL_DEPTH 1
+#endif
+constexpr int kDepth = MIATTN_PREFILL_DEPTH;
 
 __device__ __forceinline__ floatx16 zero16() {
   floatx16 z;
@@ -54,54 +70,75 @@ __device__ __forceinline__ floatx16 mfma32(const uint4& a, const uint4& b, const
   }
 }
 
+// Two fp32 values -> one word of two 16-bit values, round to nearest even; one
+// v_cvt_pk_bf16_f32 on gfx950 for bf16.
 template <typename T>
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  return uint32_t(from_f32<T>(lo).bits) | (uint32_t(from_f32<T>(hi).bits) << 16);
+  if constexpr (std::is_same<T, bf16_t>::value) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+  } else {
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    const f16x2_t v = {(_Float16)lo, (_Float16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+  }
 }
 
-// Rows of the query tile owned by one workgroup.
-template <int HPW>
-struct TileShape {
-  static constexpr int WPH = 4 / HPW;  // waves per head
-  static constexpr int RW = 32 * WPH;  // query rows per workgroup tile
-};
+// V^T tile: D rows of kBK keys (128 B = 8 slots of 16 B), no padding. Within each 16-key
+// MFMA step the 4-key groups are stored in the order [0, 2, 1, 3], so the 8 keys one lane
+// feeds to the PV MFMA (keys 4g..4g+3 and 8+4g..8+4g+3 of the step, the score
+// accumulator's layout) are one contiguous 16-byte slot; slots are XOR-swizzled by row so
+// the transposing 8-byte writes are at most 2-way bank-conflicted and the 16-byte operand
+// reads are conflict-free.
+__device__ __forceinline__ int vt_offset(int d, int grp) {  // element offset of a 4-key group
+  const int gp = (grp & ~3) | ((grp & 1) << 1) | ((grp >> 1) & 1);
+  const int slot = (gp >> 1) ^ ((d ^ (d >> 3)) & 7);
+  return d * kBK + slot * 8 + (gp & 1) * 4;
+}
 
 template <int D>
-struct KeyTile {
-  static constexpr int BN = D <= 128 ? 64 : 32;  // keys per K/V tile
+struct Tiles {
+  static constexpr int KST = D + 8;       // K tile row stride (elements): 16 B skew per row
+  static constexpr int KTILE = kBK * KST; // elements
+  static constexpr int VTILE = D * kBK;
+  static constexpr int BUF = KTILE + VTILE;
+  static constexpr int KCH = kBK * D / 8 / kThreads;          // 16-byte K chunks per thread
+  static constexpr int VPAIRS = (kBK / 4) * (D / 8);          // (4 keys x 8 d) blocks of V
+  static constexpr int VPT = (VPAIRS + kThreads - 1) / kThreads;  // blocks per thread
+  static_assert(KCH >= 1 && (kBK * D / 8) % kThreads == 0, "K staging assumes whole chunks");
 };
 
-template <typename T, int D, int HPW>
-__global__ __launch_bounds__(kThreads, 2) void varlen_prefill_kernel(
+template <typename T, int D>
+__global__ __launch_bounds__(kThreads, D <= 128 ? 2 : 1) void varlen_prefill_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     T* __restrict__ out, const int32_t* __restrict__ cu, const int32_t* __restrict__ sched,
     int H, int H_kv, int G, float scale_log2, int causal) {
-  constexpr int WPH = TileShape<HPW>::WPH;
-  constexpr int RW = TileShape<HPW>::RW;
-  constexpr int BN = KeyTile<D>::BN;
-  constexpr int KST = D + 8;   // LDS row stride of the K tile (elements)
-  constexpr int VST = BN + 8;  // LDS row stride of the transposed V tile
-  constexpr int KS = D / 16;   // MFMA k-steps over D for S^T
-  constexpr int MB = BN / 32;  // 32-key blocks per tile
-  constexpr int TS = BN / 16;  // 16-key MFMA k-steps for O^T
-  constexpr int DB = D / 32;   // 32-wide blocks of D for O^T
-  __shared__ uint16_t Ks[BN * KST];
-  __shared__ uint16_t Vt[D * VST];
+  using Tl = Tiles<D>;
+  constexpr int KS = D / 16;  // MFMA k-steps over D for S^T
+  constexpr int DB = D / 32;  // 32-row blocks of D for O^T
+  constexpr int KST = Tl::KST;
+  __shared__ __align__(16) uint16_t lds[2 * Tl::BUF];
 
-  const int hg = blockIdx.x;
+  // Head permutation: x -> h so that x % 8 (the XCD) selects a block of consecutive heads.
+  const int x = blockIdx.x;
+  const int h = (H % kXcds == 0) ? (x % kXcds) * (H / kXcds) + x / kXcds : x;
+  const int kvh = h / G;
   const int entry = sched[blockIdx.y];
-  const int seq = entry >> 16;
+  const int seq = int(uint32_t(entry) >> 16);
   const int tile = entry & 0xffff;
   const int seq0 = cu[seq];
   const int L = cu[seq + 1] - seq0;
 
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int g = lane >> 5;     // which half of the wave (k-group of the MFMA operands)
-  const int col = lane & 31;   // query column owned by this lane
-  const int h = hg * HPW + wave / WPH;
-  const int kvh = (hg * HPW) / G;
-  const int qi = tile * RW + (wave % WPH) * 32 + col;  // local query index
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int qb = wave & 1;    // query block of this wave
+  const int kh = wave >> 1;   // key half of every tile
+  const int g = lane >> 5;    // k-group of the MFMA operands
+  const int col = lane & 31;  // query column owned by this lane
+  const int qrow0 = tile * kBQ + qb * 32;
+  const int qi = qrow0 + col;  // local query index
 
   const int64_t q_row = int64_t(H) * D;
   const int64_t kv_row = int64_t(H_kv) * D;
@@ -110,10 +147,108 @@ __global__ __launch_bounds__(kThreads, 2) void varlen_prefill_kernel(
   uint4 qB[KS];
   {
     const int qc = qi < L ? qi : L - 1;
-    const T* qp = q + (seq0 + qc) * q_row + h * D + g * 8;
+    const T* qp = q + int64_t(seq0 + qc) * q_row + h * D + g * 8;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) qB[ks] = load16(qp + ks * 16);
   }
+
+  // Loop-invariant LDS offsets of this lane's V^T operand slots (keys kh*32 + 16t +
+  // {4g..4g+3, 8+4g..8+4g+3} of D row db*32 + col; see vt_offset).
+  int vt_rd[DB][2];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) vt_rd[db][t] = vt_offset(db * 32 + col, kh * 8 + t * 4 + g);
+  }
+
+  const int q_end = min(L, tile * kBQ + kBQ);
+  const int n_it = causal ? (q_end + kBK - 1) / kBK : (L + kBK - 1) / kBK;
+
+  // ---- tile staging: global -> registers (issued early) -> LDS (after the MFMAs)
+  uint4 kreg[kDepth][Tl::KCH];
+  uint4 vreg[kDepth][Tl::VPT][4];
+  // K/V tiles are read with buffer loads: one scalar resource per tile whose base is the
+  // tile's first token and whose size ends at the segment's last token, so each lane's
+  // byte offset is a constant for the whole loop and keys past the segment read as zero
+  // (range-checked by the hardware; they are masked out of the softmax anyway).
+  const int row_b = int(kv_row) * 2;  // bytes per packed token (all KV heads)
+  int koff[Tl::KCH];
+#pragma unroll
+  for (int c = 0; c < Tl::KCH; ++c) {
+    const int idx = c * kThreads + tid;
+    const int key = idx / (D / 8), cc = idx - key * (D / 8);
+    koff[c] = key * row_b + kvh * D * 2 + cc * 16;
+  }
+  int voff[Tl::VPT];
+#pragma unroll
+  for (int p = 0; p < Tl::VPT; ++p) {
+    const int pr = p * kThreads + tid;
+    const int kq = pr / (D / 8), dq = pr - kq * (D / 8);
+    voff[p] = kq * 4 * row_b + kvh * D * 2 + dq * 16;
+  }
+  auto tile_rsrc = [&](const T* base, int key0) {
+    return __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<T*>(base + int64_t(seq0 + key0) * kv_row), (short)0, (L - key0) * row_b,
+        0x00020000);
+  };
+  // The register set is a compile-time index: a runtime index would make the compiler
+  // select between the sets right after each load and wait for the data there.
+  auto load_tile = [&](int it, auto set_c) {
+    constexpr int set = decltype(set_c)::value;
+    const int key0 = it * kBK;
+    const auto rk = tile_rsrc(k, key0);
+    const auto rv = tile_rsrc(v, key0);
+#pragma unroll
+    for (int c = 0; c < Tl::KCH; ++c) {
+      kreg[set][c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, koff[c], 0, 0));
+    }
+#pragma unroll
+    for (int p = 0; p < Tl::VPT; ++p) {
+      const int pr = p * kThreads + tid;
+      if (Tl::VPAIRS % kThreads == 0 || pr < Tl::VPAIRS) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          vreg[set][p][j] = __builtin_bit_cast(
+              uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, voff[p] + j * row_b, 0, 0));
+        }
+      }
+    }
+  };
+  auto store_tile = [&](int buf, auto set_c) {
+    constexpr int set = decltype(set_c)::value;
+    uint16_t* Ks = lds + buf * Tl::BUF;
+    uint16_t* Vt = Ks + Tl::KTILE;
+#pragma unroll
+    for (int c = 0; c < Tl::KCH; ++c) {
+      const int idx = c * kThreads + tid;
+      const int key = idx / (D / 8), cc = idx - key * (D / 8);
+      *reinterpret_cast<uint4*>(&Ks[key * KST + cc * 8]) = kreg[set][c];
+    }
+#pragma unroll
+    for (int p = 0; p < Tl::VPT; ++p) {
+      const int pr = p * kThreads + tid;
+      if (Tl::VPAIRS % kThreads == 0 || pr < Tl::VPAIRS) {
+        const int kq = pr / (D / 8), dq = pr - kq * (D / 8);
+        const uint4* vr = vreg[set][p];
+        const uint32_t w[4][4] = {{vr[0].x, vr[0].y, vr[0].z, vr[0].w},
+                                  {vr[1].x, vr[1].y, vr[1].z, vr[1].w},
+                                  {vr[2].x, vr[2].y, vr[2].z, vr[2].w},
+                                  {vr[3].x, vr[3].y, vr[3].z, vr[3].w}};
+        // word m of key j holds d = 2m (low half) and 2m+1 (high half); V^T row d gets
+        // the four keys' values of d as two words.
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const uint2 even = make_uint2((w[0][m] & 0xffffu) | (w[1][m] << 16),
+                                        (w[2][m] & 0xffffu) | (w[3][m] << 16));
+          const uint2 odd = make_uint2((w[0][m] >> 16) | (w[1][m] & 0xffff0000u),
+                                       (w[2][m] >> 16) | (w[3][m] & 0xffff0000u));
+          const int d0 = dq * 8 + 2 * m;
+          *reinterpret_cast<uint2*>(&Vt[vt_offset(d0, kq)]) = even;
+          *reinterpret_cast<uint2*>(&Vt[vt_offset(d0 + 1, kq)]) = odd;
+        }
+      }
+    }
+  };
 
   floatx16 o[DB];
 #pragma unroll
@@ -121,160 +256,189 @@ __global__ __launch_bounds__(kThreads, 2) void varlen_prefill_kernel(
   float m_i = -INFINITY;
   float l_i = 0.0f;
 
-  const int tile_end = min(L, tile * RW + RW);
-  const int n_kt = causal ? (tile_end + BN - 1) / BN : (L + BN - 1) / BN;
-  const T* kseg = k + int64_t(seq0) * kv_row + kvh * D;
-  const T* vseg = v + int64_t(seq0) * kv_row + kvh * D;
-
-  for (int kt = 0; kt < n_kt; ++kt) {
-    const int key0 = kt * BN;
-    __syncthreads();
-    // Stage K row-major: consecutive threads read consecutive 16-byte chunks of a row.
-    for (int idx = threadIdx.x; idx < BN * D / 8; idx += kThreads) {
-      const int key = idx / (D / 8);
-      const int cch = idx - key * (D / 8);
-      const int tok = key0 + key;
-      const uint4 val = tok < L ? load16(kseg + tok * kv_row + cch * 8) : make_uint4(0, 0, 0, 0);
-      *reinterpret_cast<uint4*>(&Ks[key * KST + cch * 8]) = val;
-    }
-    // Stage V transposed (Vt[d][key]): consecutive threads take consecutive keys so the
-    // 2-byte LDS stores of one wave land on consecutive addresses.
-    for (int idx = threadIdx.x; idx < BN * D / 8; idx += kThreads) {
-      const int key = idx % BN;
-      const int cch = idx / BN;
-      const int tok = key0 + key;
-      const uint4 val = tok < L ? load16(vseg + tok * kv_row + cch * 8) : make_uint4(0, 0, 0, 0);
-      const uint32_t w[4] = {val.x, val.y, val.z, val.w};
+  // Tile it+1 and it+2 are in flight in the two register sets while tile it is computed
+  // from LDS; tile it+1 is written to the other LDS buffer after the MFMAs.
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  load_tile(0, S0{});
+  store_tile(0, S0{});
+  // Consume the Q fragments here, before the loop: otherwise their loads can still be in
+  // flight at the loop header, and the in-order load counter then makes every score MFMA
+  // of every tile wait for that tile's K/V prefetch. (An empty asm that reads the
+  // registers; the compiler places the wait for the Q loads in front of it.)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        Vt[(cch * 8 + e) * VST + key] = uint16_t((w[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
-      }
-    }
-    __syncthreads();
+  for (int ks = 0; ks < KS; ++ks) asm volatile("" ::"v"(qB[ks].x), "v"(qB[ks].y), "v"(qB[ks].z), "v"(qB[ks].w));
+  if constexpr (kDepth == 2) {
+    if (n_it > 1) load_tile(1, S1{});
+    if (n_it > 2) load_tile(2, S0{});
+  }
+  __syncthreads();
 
-    // S^T[key][query] for the MB 32-key blocks of the tile.
-    floatx16 sacc[MB];
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      sacc[mb] = zero16();
+  // One tile: compute tile `it` from LDS buffer it & 1 while tile it+1 (and, at depth 2,
+  // it+2) is in flight in registers, then move tile it+1 into the other buffer. At depth 2
+  // the register set (it+1) & 1 is then reused for tile it+3.
+  auto step = [&](int it, auto set_c) {
+    const bool more = it + 1 < n_it;
+    if constexpr (kDepth == 1) {
+      if (more) load_tile(it + 1, S0{});
+    }
+    const int kb0 = it * kBK + kh * 32;  // first key of this wave's half
+    const bool live = kb0 < L && !(causal && kb0 > qrow0 + 31);
+    if (live) {
+      const uint16_t* Ks = lds + (it & 1) * Tl::BUF;
+      const uint16_t* Vt = Ks + Tl::KTILE;
+      // S^T[key][query] for the wave's 32 keys: all K fragments first, then the MFMAs.
+      uint4 kf[KS];
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const uint4 a = *reinterpret_cast<const uint4*>(&Ks[(mb * 32 + col) * KST + ks * 16 + g * 8]);
-        sacc[mb] = mfma32<T>(a, qB[ks], sacc[mb]);
+        kf[ks] = *reinterpret_cast<const uint4*>(&Ks[(kh * 32 + col) * KST + ks * 16 + g * 8]);
       }
-    }
-
-    // Scale, mask, online softmax for this lane's query column.
-    float mloc = -INFINITY;
+      floatx16 sacc = zero16();
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
+      for (int ks = 0; ks < KS; ++ks) sacc = mfma32<T>(kf[ks], qB[ks], sacc);
+      // V^T fragments of the PV product, read now so they arrive during the softmax.
+      uint4 vf[DB][2];
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) vf[db][t] = *reinterpret_cast<const uint4*>(&Vt[vt_rd[db][t]]);
+      }
+      // Online softmax for this lane's query column, in raw score units: the scale is
+      // applied once to the max and folded into the exp2 argument (one FMA per score).
+      // Only boundary tiles (segment end, causal diagonal) need the mask.
+      const bool interior = kb0 + 31 < L && !(causal && kb0 + 31 > qrow0);
+      if (!interior) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int key = kb0 + (j >> 2) * 8 + g * 4 + (j & 3);
+          if (key >= L || (causal && key > qi)) sacc[j] = -INFINITY;
+        }
+      }
+      float mloc = sacc[0];
+#pragma unroll
+      for (int j = 1; j < 16; ++j) mloc = fmaxf(mloc, sacc[j]);
+      const float m_tile = fmaxf(mloc, swap32(mloc)) * scale_log2;
+      const float m_new = fmaxf(m_i, m_tile);
+      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+      // Rescale the accumulators only when some lane's running max moved (a wave-wide
+      // vote); with a settled max the 4*DB*4 multiplies are skipped.
+      if (__any(m_new != m_i)) {
+        const float alpha = fast_exp2(m_i - m_use);
+        l_i *= alpha;
+#pragma unroll
+        for (int i = 0; i < DB; ++i) o[i] *= alpha;
+      }
+      m_i = m_new;
+      float lsum = 0.0f;
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        const int key = key0 + mb * 32 + (j >> 2) * 8 + g * 4 + (j & 3);
-        const bool masked = key >= L || (causal && key > qi);
-        const float s = masked ? -INFINITY : sacc[mb][j] * scale_log2;
-        sacc[mb][j] = s;
-        mloc = fmaxf(mloc, s);
-      }
-    }
-    const float m_tile = fmaxf(mloc, swap32(mloc));
-    const float m_new = fmaxf(m_i, m_tile);
-    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    const float alpha = fast_exp2(m_i - m_use);
-    m_i = m_new;
-    float lsum = 0.0f;
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const float p = fast_exp2(sacc[mb][j] - m_use);
-        sacc[mb][j] = p;
+        const float p = fast_exp2(fmaf(sacc[j], scale_log2, -m_use));
+        sacc[j] = p;
         lsum += p;
       }
-    }
-    l_i = l_i * alpha + lsum;
+      l_i += lsum;
+      // P^T as the B operand: k-step t covers keys 16t..16t+15 and the lane's 8 values are
+      // sacc[8t .. 8t+8] (keys 4g+0..3 and 8+4g+0..3 of that step).
+      uint4 pB[2];
 #pragma unroll
-    for (int i = 0; i < DB; ++i) o[i] *= alpha;
-
-    // P^T as the B operand of O^T += V^T P^T: k-step t covers keys 16t..16t+15 and the
-    // lane's 8 values are sacc[t/2][(t%2)*8 .. +8] (keys 4g+0..3 and 8+4g+0..3).
-    uint4 pB[TS];
-#pragma unroll
-    for (int t = 0; t < TS; ++t) {
-      const int mb = t >> 1, jb = (t & 1) * 8;
-      pB[t] = make_uint4(pack2<T>(sacc[mb][jb + 0], sacc[mb][jb + 1]),
-                         pack2<T>(sacc[mb][jb + 2], sacc[mb][jb + 3]),
-                         pack2<T>(sacc[mb][jb + 4], sacc[mb][jb + 5]),
-                         pack2<T>(sacc[mb][jb + 6], sacc[mb][jb + 7]));
-    }
-#pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      const uint16_t* vrow = &Vt[(db * 32 + col) * VST + g * 4];
-#pragma unroll
-      for (int t = 0; t < TS; ++t) {
-        const uint2 lo = *reinterpret_cast<const uint2*>(vrow + t * 16);
-        const uint2 hi = *reinterpret_cast<const uint2*>(vrow + t * 16 + 8);
-        o[db] = mfma32<T>(make_uint4(lo.x, lo.y, hi.x, hi.y), pB[t], o[db]);
+      for (int t = 0; t < 2; ++t) {
+        pB[t] = make_uint4(pack2<T>(sacc[8 * t + 0], sacc[8 * t + 1]),
+                           pack2<T>(sacc[8 * t + 2], sacc[8 * t + 3]),
+                           pack2<T>(sacc[8 * t + 4], sacc[8 * t + 5]),
+                           pack2<T>(sacc[8 * t + 6], sacc[8 * t + 7]));
       }
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) o[db] = mfma32<T>(vf[db][t], pB[t], o[db]);
+      }
+    }
+    if (more) {
+      if constexpr (kDepth == 1) {
+        store_tile((it + 1) & 1, S0{});
+      } else {
+        store_tile((it + 1) & 1, set_c);
+        if (it + 3 < n_it) load_tile(it + 3, set_c);
+      }
+    }
+    __syncthreads();
+  };
+  if constexpr (kDepth == 1) {
+    for (int it = 0; it < n_it; ++it) step(it, S0{});
+  } else {
+    for (int it = 0; it < n_it; it += 2) {
+      step(it, S1{});
+      if (it + 1 < n_it) step(it + 1, S0{});
     }
   }
 
-  // Normalise and store: lane owns query qi and, per 32-wide D block, d values
-  // (j/4)*8 + 4g + (j%4) -> four runs of 4 consecutive elements.
+  // Fold the two key halves of each query block: the kh = 1 waves publish (m, l, O^T)
+  // through LDS, the kh = 0 waves merge, normalise and store.
   const float l_tot = l_i + swap32(l_i);
-  const float inv = 1.0f / fmaxf(l_tot, 1e-30f);
-  if (qi < L) {
-    T* op = out + (seq0 + qi) * q_row + h * D;
+  float* mbuf = reinterpret_cast<float*>(lds);  // [qb][DB*16 + 2][64]
+  constexpr int NE = DB * 16 + 2;
+  float* mine = mbuf + qb * NE * 64;
+  if (kh == 1) {
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
 #pragma unroll
+      for (int j = 0; j < 16; ++j) mine[(db * 16 + j) * 64 + lane] = o[db][j];
+    }
+    mine[(DB * 16) * 64 + lane] = m_i;
+    mine[(DB * 16 + 1) * 64 + lane] = l_tot;
+  }
+  __syncthreads();
+  if (kh == 1) return;
+  const float m1 = mine[(DB * 16) * 64 + lane];
+  const float l1 = mine[(DB * 16 + 1) * 64 + lane];
+  const float M = fmaxf(m_i, m1);
+  const float M_use = M == -INFINITY ? 0.0f : M;
+  const float w0 = fast_exp2(m_i - M_use);
+  const float w1 = fast_exp2(m1 - M_use);
+  const float inv = 1.0f / fmaxf(l_tot * w0 + l1 * w1, 1e-30f);
+  if (qi < L) {
+    T* op = out + int64_t(seq0 + qi) * q_row + h * D;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      float r[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) r[j] = (o[db][j] * w0 + mine[(db * 16 + j) * 64 + lane] * w1) * inv;
+      // lane owns query qi and, per 32-wide D block, d = (j/4)*8 + 4g + (j%4): four runs
+      // of 4 consecutive elements.
+#pragma unroll
       for (int jg = 0; jg < 4; ++jg) {
         const int d = db * 32 + jg * 8 + g * 4;
-        const uint2 val = make_uint2(pack2<T>(o[db][jg * 4 + 0] * inv, o[db][jg * 4 + 1] * inv),
-                                     pack2<T>(o[db][jg * 4 + 2] * inv, o[db][jg * 4 + 3] * inv));
+        const uint2 val = make_uint2(pack2<T>(r[jg * 4 + 0], r[jg * 4 + 1]),
+                                     pack2<T>(r[jg * 4 + 2], r[jg * 4 + 3]));
         *reinterpret_cast<uint2*>(op + d) = val;
       }
     }
   }
 }
 
-int hpw_for(int G) { return (G % 4 == 0) ? 4 : (G % 2 == 0) ? 2 : 1; }
+int rows_per_tile() { return kBQ; }
 
-int rows_per_tile(int G) { return 32 * (4 / hpw_for(G)); }
+int keys_per_tile() { return kBK; }
 
-int keys_per_tile(int D) { return D <= 128 ? 64 : 32; }
-
-template <typename T, int D, int HPW>
-int launch3(const void* q, const void* k, const void* v, void* out, const int32_t* cu,
+template <typename T, int D>
+int launch2(const void* q, const void* k, const void* v, void* out, const int32_t* cu,
             const int32_t* sched, int n_tiles, int H, int H_kv, float scale_log2, int causal,
             hipStream_t s) {
-  dim3 grid(H / HPW, n_tiles);
-  hipLaunchKernelGGL((varlen_prefill_kernel<T, D, HPW>), grid, dim3(kThreads), 0, s,
+  dim3 grid(H, n_tiles);
+  hipLaunchKernelGGL((varlen_prefill_kernel<T, D>), grid, dim3(kThreads), 0, s,
                      static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
                      static_cast<T*>(out), cu, sched, H, H_kv, H / H_kv, scale_log2, causal);
   return launch_status("mi_varlen_prefill");
 }
 
-template <typename T, int D>
-int launch2(int hpw, const void* q, const void* k, const void* v, void* out, const int32_t* cu,
+template <typename T>
+int launch1(int D, const void* q, const void* k, const void* v, void* out, const int32_t* cu,
             const int32_t* sched, int n_tiles, int H, int H_kv, float sl2, int causal,
             hipStream_t s) {
-  switch (hpw) {
-    case 1: return launch3<T, D, 1>(q, k, v, out, cu, sched, n_tiles, H, H_kv, sl2, causal, s);
-    case 2: return launch3<T, D, 2>(q, k, v, out, cu, sched, n_tiles, H, H_kv, sl2, causal, s);
-    case 4: return launch3<T, D, 4>(q, k, v, out, cu, sched, n_tiles, H, H_kv, sl2, causal, s);
-  }
-  return fail(MI_ERR_UNSUPPORTED, "mi_varlen_prefill: bad heads-per-workgroup %d", hpw);
-}
-
-template <typename T>
-int launch1(int D, int hpw, const void* q, const void* k, const void* v, void* out,
-            const int32_t* cu, const int32_t* sched, int n_tiles, int H, int H_kv, float sl2,
-            int causal, hipStream_t s) {
   switch (D) {
-    case 64: return launch2<T, 64>(hpw, q, k, v, out, cu, sched, n_tiles, H, H_kv, sl2, causal, s);
-    case 128: return launch2<T, 128>(hpw, q, k, v, out, cu, sched, n_tiles, H, H_kv, sl2, causal, s);
-    case 256: return launch2<T, 256>(hpw, q, k, v, out, cu, sched, n_tiles, H, H_kv, sl2, causal, s);
+    case 64: return launch2<T, 64>(q, k, v, out, cu, sched, n_tiles, H, H_kv, sl2, causal, s);
+    case 128: return launch2<T, 128>(q, k, v, out, cu, sched, n_tiles, H, H_kv, sl2, causal, s);
+    case 256: return launch2<T, 256>(q, k, v, out, cu, sched, n_tiles, H, H_kv, sl2, causal, s);
   }
   return fail(MI_ERR_UNSUPPORTED,
               "mi_varlen_prefill: head_dim %d is not supported by the HIP prefill kernel "
@@ -295,8 +459,9 @@ extern "C" int mi_varlen_schedule(const int32_t* host_cu_seqlens, int n_seqs, in
     return fail(MI_ERR_INVALID, "mi_varlen_schedule: n_head (%d) must be a multiple of n_kv_head (%d)",
                 H, H_kv);
   }
-  const int RW = rows_per_tile(H / H_kv);
-  const int BN = keys_per_tile(D);
+  (void)D;
+  const int RW = rows_per_tile();
+  const int BN = keys_per_tile();
   struct Item { int work, seq, tile; };
   std::vector<Item> items;
   for (int s = 0; s < n_seqs; ++s) {
@@ -348,13 +513,12 @@ extern "C" int mi_varlen_prefill(const void* q, const void* k, const void* v, vo
   if (!al(q) || !al(k) || !al(v) || !al(out)) {
     return fail(MI_ERR_UNSUPPORTED, "mi_varlen_prefill: q/k/v/out must be 16-byte aligned");
   }
-  const int hpw = hpw_for(H / H_kv);
   const float sl2 = float(double(scale) * 1.4426950408889634);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == MI_BF16) {
-    return launch1<bf16_t>(D, hpw, q, k, v, out, cu_seqlens, tile_schedule, n_tiles, H, H_kv, sl2,
+    return launch1<bf16_t>(D, q, k, v, out, cu_seqlens, tile_schedule, n_tiles, H, H_kv, sl2,
                            causal, s);
   }
-  return launch1<f16_t>(D, hpw, q, k, v, out, cu_seqlens, tile_schedule, n_tiles, H, H_kv, sl2,
+  return launch1<f16_t>(D, q, k, v, out, cu_seqlens, tile_schedule, n_tiles, H, H_kv, sl2,
                         causal, s);
 }

@@ -57,7 +57,7 @@ def _schedule(lengths, H=16, H_kv=8, D=128, causal=1):
 
 def test_schedule_covers_every_tile_once_heaviest_first():
     lengths = [100, 1, 700, 64, 65]
-    rows = 64  # GQA 2 -> two heads per workgroup -> 64-row query tiles
+    rows = 64  # 64 query rows per workgroup (one head, 2 query blocks x 2 key halves)
     sched = _schedule(lengths)
     expected = {(s, t) for s, n in enumerate(lengths) for t in range(-(-n // rows))}
     assert sorted(sched) == sorted(expected)
