@@ -214,6 +214,75 @@ def bench_prefill(stream, steps: int = 20, eager: bool = False):
     }
 
 
+def bench_tpot(stream, prompt_len: int = 1920, new_tokens: int = 128, B: int = 32, seed: int = 0) -> dict:
+    """Config 5 shape, closed batch: random-init Qwen3-0.6B, B rows of ``prompt_len`` random
+    tokens prefilled in one packed group, then ``new_tokens`` greedy decode steps (context
+    ``prompt_len`` -> ``prompt_len + new_tokens``). TPOT = GPU time of one whole decode step
+    (28 layers: projections, norms, RoPE, HIP slot write, HIP paged decode, MLP, lm_head,
+    argmax), replayed from one HIP graph; the eager (Python-launched) step is reported too."""
+    from miattn import PagedKV
+    from miattn.qwen3 import GraphDecoder, Qwen3, Qwen3Config, random_weights
+
+    cfg = Qwen3Config()
+    model = Qwen3(cfg, random_weights(cfg, seed), "cuda")
+    gen = torch.Generator().manual_seed(seed + 1)
+    prompts = [torch.randint(0, cfg.vocab, (prompt_len,), generator=gen).tolist() for _ in range(B)]
+    bs = 16
+    per = (prompt_len + new_tokens + 1 + bs - 1) // bs
+    n_blocks = max(8192, B * per)
+    perm = torch.randperm(n_blocks, generator=torch.Generator().manual_seed(seed + 2)).tolist()
+    tables = [perm[r * per:(r + 1) * per] for r in range(B)]
+    pool = model.new_pool(n_blocks, bs)
+    with torch.cuda.stream(stream):
+        torch.cuda.synchronize()
+        with EventTimer(stream) as t:
+            logits = model.prefill(prompts, pool, tables)
+        prefill_ms = t.ms()
+        first = logits.argmax(-1)
+        # eager steps on a copy of the state (PagedKV, Python launch path)
+        paged = PagedKV(pool, tables, [prompt_len] * B, rope_len=prompt_len + new_tokens + 1, n_head=cfg.n_head)
+        tok = first
+        for _ in range(2):
+            tok = model.decode(paged, tok).argmax(-1)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(8):
+            tok = model.decode(paged, tok).argmax(-1)
+        torch.cuda.synchronize()
+        eager_ms = (time.perf_counter() - t0) * 1e3 / 8
+    dec = GraphDecoder(model, pool, tables, [prompt_len] * B, first, new_tokens)
+    dec.capture(stream)
+    samples = []
+    with torch.cuda.stream(stream):
+        torch.cuda.synchronize()
+        with EventTimer(stream) as total:
+            for _ in range(new_tokens):
+                dec.step()
+        total_ms = total.ms()
+    # second pass over the same positions, one event pair per step, for percentiles
+    dec.pos.fill_(prompt_len)
+    dec.tokens.copy_(first)
+    dec.step_idx.zero_()
+    with torch.cuda.stream(stream):
+        for _ in range(new_tokens):
+            with EventTimer(stream) as t:
+                dec.step()
+            samples.append(t.ms())
+    torch.cuda.synchronize()
+    return {
+        "workload": f"config5 shape (closed batch): random-init Qwen3-0.6B bf16, B={B}, prompt {prompt_len} "
+                    f"random tokens, {new_tokens} greedy steps (context {prompt_len}->{prompt_len + new_tokens}), "
+                    "block 16, decode step replayed from one HIP graph",
+        "tpot_ms": total_ms / new_tokens,
+        "tpot_p50_ms": percentile(samples, 0.5),
+        "tpot_p95_ms": percentile(samples, 0.95),
+        "decode_tokens_per_s": B * new_tokens / (total_ms * 1e-3),
+        "eager_step_ms": eager_ms,
+        "prefill_ms": prefill_ms,
+        "prefill_tokens": B * prompt_len,
+    }
+
+
 def copy_calibration(mib: int, reps: int) -> dict:
     """A plain device copy of a known size, run under the same PMC counters as the decode
     kernel: FETCH_SIZE / WRITE_SIZE of this launch over its known bytes is the counters'
@@ -308,6 +377,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--decode-only", action="store_true", help="only the headline decode leg (for profiling)")
+    ap.add_argument("--e2e-only", action="store_true", help="only the end-to-end TPOT leg")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the config-3 prefill and slot-write legs (for profiling)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -334,6 +404,9 @@ def main() -> int:
         print(json.dumps(copy_calibration(args.copy_calibration, 5)), flush=True)
         return 0
     stream = torch.cuda.Stream()
+    if args.e2e_only:
+        print(json.dumps({"e2e": bench_tpot(stream)}), flush=True)
+        return 0
     if args.prefill_only:
         print(json.dumps({"prefill": bench_prefill(stream, args.steps, eager=args.eager)}), flush=True)
         return 0
@@ -385,6 +458,11 @@ def main() -> int:
         line["prefill"] = bench_prefill(stream)
         log(f"prefill: {line['prefill']['prefill_tflops']:.1f} TFLOP/s, "
             f"slot write {line['prefill']['slot_write_gbs']:.1f} GB/s")
+        log("end-to-end TPOT (config 5 shape, B=32 ctx 2048)")
+        line["e2e"] = bench_tpot(stream)
+        line["tpot_ms"] = round(line["e2e"]["tpot_ms"], 4)
+        log(f"TPOT {line['tpot_ms']:.3f} ms (eager step {line['e2e']['eager_step_ms']:.2f} ms)")
+        torch.cuda.empty_cache()
         log("long-context decode (config 4)")
         line["long_context"] = bench_long_context(stream)
         log(f"config4: {line['long_context']['gbs']:.1f} GB/s")

@@ -40,9 +40,7 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
 
-constexpr int kThreads = 256;
-constexpr int kBQ = 64;  // query rows per workgroup
-constexpr int kBK = 64;  // keys per tile (two halves of 32)
+constexpr int kBQ = 64;  // query rows per workgroup (two blocks of 32)
 constexpr int kXcds = 8; // MI355X: 8 XCDs, workgroups dispatched round-robin over them
 
 // K/V tiles in flight in registers while a tile is computed: 1 (tile it+1) or 2 (it+1 and
@@ -85,36 +83,49 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
   }
 }
 
-// V^T tile: D rows of kBK keys (128 B = 8 slots of 16 B), no padding. Within each 16-key
+// V^T tile: D rows of BK keys (BK/8 slots of 16 B), no padding. Within each 16-key
 // MFMA step the 4-key groups are stored in the order [0, 2, 1, 3], so the 8 keys one lane
 // feeds to the PV MFMA (keys 4g..4g+3 and 8+4g..8+4g+3 of the step, the score
 // accumulator's layout) are one contiguous 16-byte slot; slots are XOR-swizzled by row so
 // the transposing 8-byte writes are at most 2-way bank-conflicted and the 16-byte operand
 // reads are conflict-free.
+template <int BK>
 __device__ __forceinline__ int vt_offset(int d, int grp) {  // element offset of a 4-key group
   const int gp = (grp & ~3) | ((grp & 1) << 1) | ((grp >> 1) & 1);
   const int slot = (gp >> 1) ^ ((d ^ (d >> 3)) & 7);
-  return d * kBK + slot * 8 + (gp & 1) * 4;
+  return d * BK + slot * 8 + (gp & 1) * 4;
 }
 
+// NKS waves share each query block, each taking 32 keys of a BK = 32*NKS tile, so the
+// serial chain of the longest causal tile is L / (32*NKS) tiles. NKS = 2 (4 waves, two
+// 64-key LDS buffers, 2 workgroups per CU at D = 128) measured faster on config 3 than
+// NKS = 4 (8 waves, 128-key tiles, one workgroup per CU: 57.6 vs 39.5 us per layer),
+// because two independent workgroups overlap each other's barrier and staging phases.
+#ifndef MIATTN_PREFILL_NKS
+#define MIATTN_PREFILL_NKS 2
+#endif
 template <int D>
 struct Tiles {
-  static constexpr int KST = D + 8;       // K tile row stride (elements): 16 B skew per row
-  static constexpr int KTILE = kBK * KST; // elements
-  static constexpr int VTILE = D * kBK;
+  static constexpr int NKS = D <= 128 ? MIATTN_PREFILL_NKS : 2;  // key splits per tile
+  static constexpr int THREADS = 64 * 2 * NKS;  // 2 query blocks x NKS key splits
+  static constexpr int BK = 32 * NKS;           // keys per tile
+  static constexpr int KST = D + 8;             // K tile row stride (elements): 16 B skew
+  static constexpr int KTILE = BK * KST;        // elements
+  static constexpr int VTILE = D * BK;
   static constexpr int BUF = KTILE + VTILE;
-  static constexpr int KCH = kBK * D / 8 / kThreads;          // 16-byte K chunks per thread
-  static constexpr int VPAIRS = (kBK / 4) * (D / 8);          // (4 keys x 8 d) blocks of V
-  static constexpr int VPT = (VPAIRS + kThreads - 1) / kThreads;  // blocks per thread
-  static_assert(KCH >= 1 && (kBK * D / 8) % kThreads == 0, "K staging assumes whole chunks");
+  static constexpr int KCH = BK * D / 8 / THREADS;                 // 16-byte K chunks per thread
+  static constexpr int VPAIRS = (BK / 4) * (D / 8);                // (4 keys x 8 d) blocks of V
+  static constexpr int VPT = (VPAIRS + THREADS - 1) / THREADS;     // blocks per thread
+  static_assert(KCH >= 1 && (BK * D / 8) % THREADS == 0, "K staging assumes whole chunks");
 };
 
 template <typename T, int D>
-__global__ __launch_bounds__(kThreads, D <= 128 ? 2 : 1) void varlen_prefill_kernel(
+__global__ __launch_bounds__(Tiles<D>::THREADS, D <= 128 && Tiles<D>::NKS == 2 ? 2 : 1) void varlen_prefill_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     T* __restrict__ out, const int32_t* __restrict__ cu, const int32_t* __restrict__ sched,
     int H, int H_kv, int G, float scale_log2, int causal) {
   using Tl = Tiles<D>;
+  constexpr int kThreads = Tl::THREADS, kBK = Tl::BK, NKS = Tl::NKS;
   constexpr int KS = D / 16;  // MFMA k-steps over D for S^T
   constexpr int DB = D / 32;  // 32-row blocks of D for O^T
   constexpr int KST = Tl::KST;
@@ -134,7 +145,7 @@ __global__ __launch_bounds__(kThreads, D <= 128 ? 2 : 1) void varlen_prefill_ker
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int qb = wave & 1;    // query block of this wave
-  const int kh = wave >> 1;   // key half of every tile
+  const int kh = wave >> 1;   // key split (32 keys) of every tile
   const int g = lane >> 5;    // k-group of the MFMA operands
   const int col = lane & 31;  // query column owned by this lane
   const int qrow0 = tile * kBQ + qb * 32;
@@ -158,7 +169,7 @@ __global__ __launch_bounds__(kThreads, D <= 128 ? 2 : 1) void varlen_prefill_ker
 #pragma unroll
   for (int db = 0; db < DB; ++db) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t) vt_rd[db][t] = vt_offset(db * 32 + col, kh * 8 + t * 4 + g);
+    for (int t = 0; t < 2; ++t) vt_rd[db][t] = vt_offset<kBK>(db * 32 + col, kh * 8 + t * 4 + g);
   }
 
   const int q_end = min(L, tile * kBQ + kBQ);
@@ -243,8 +254,8 @@ __global__ __launch_bounds__(kThreads, D <= 128 ? 2 : 1) void varlen_prefill_ker
           const uint2 odd = make_uint2((w[0][m] >> 16) | (w[1][m] & 0xffff0000u),
                                        (w[2][m] >> 16) | (w[3][m] & 0xffff0000u));
           const int d0 = dq * 8 + 2 * m;
-          *reinterpret_cast<uint2*>(&Vt[vt_offset(d0, kq)]) = even;
-          *reinterpret_cast<uint2*>(&Vt[vt_offset(d0 + 1, kq)]) = odd;
+          *reinterpret_cast<uint2*>(&Vt[vt_offset<kBK>(d0, kq)]) = even;
+          *reinterpret_cast<uint2*>(&Vt[vt_offset<kBK>(d0 + 1, kq)]) = odd;
         }
       }
     }
@@ -282,7 +293,7 @@ __global__ __launch_bounds__(kThreads, D <= 128 ? 2 : 1) void varlen_prefill_ker
     if constexpr (kDepth == 1) {
       if (more) load_tile(it + 1, S0{});
     }
-    const int kb0 = it * kBK + kh * 32;  // first key of this wave's half
+    const int kb0 = it * kBK + kh * 32;  // first key of this wave's split
     const bool live = kb0 < L && !(causal && kb0 > qrow0 + 31);
     if (live) {
       const uint16_t* Ks = lds + (it & 1) * Tl::BUF;
@@ -372,13 +383,13 @@ __global__ __launch_bounds__(kThreads, D <= 128 ? 2 : 1) void varlen_prefill_ker
     }
   }
 
-  // Fold the two key halves of each query block: the kh = 1 waves publish (m, l, O^T)
-  // through LDS, the kh = 0 waves merge, normalise and store.
+  // Fold the NKS key splits of each query block: the waves with kh > 0 publish
+  // (m, l, O^T) through LDS, the kh = 0 waves merge, normalise and store.
   const float l_tot = l_i + swap32(l_i);
-  float* mbuf = reinterpret_cast<float*>(lds);  // [qb][DB*16 + 2][64]
   constexpr int NE = DB * 16 + 2;
-  float* mine = mbuf + qb * NE * 64;
-  if (kh == 1) {
+  float* mbuf = reinterpret_cast<float*>(lds);  // [qb][kh-1][NE][64]
+  if (kh > 0) {
+    float* mine = mbuf + (qb * (NKS - 1) + kh - 1) * NE * 64;
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
 #pragma unroll
@@ -388,21 +399,33 @@ __global__ __launch_bounds__(kThreads, D <= 128 ? 2 : 1) void varlen_prefill_ker
     mine[(DB * 16 + 1) * 64 + lane] = l_tot;
   }
   __syncthreads();
-  if (kh == 1) return;
-  const float m1 = mine[(DB * 16) * 64 + lane];
-  const float l1 = mine[(DB * 16 + 1) * 64 + lane];
-  const float M = fmaxf(m_i, m1);
+  if (kh > 0) return;
+  const float* part = mbuf + qb * (NKS - 1) * NE * 64;
+  float M = m_i;
+#pragma unroll
+  for (int sp = 0; sp < NKS - 1; ++sp) M = fmaxf(M, part[(sp * NE + DB * 16) * 64 + lane]);
   const float M_use = M == -INFINITY ? 0.0f : M;
   const float w0 = fast_exp2(m_i - M_use);
-  const float w1 = fast_exp2(m1 - M_use);
-  const float inv = 1.0f / fmaxf(l_tot * w0 + l1 * w1, 1e-30f);
+  float wsp[NKS - 1];
+  float l_all = l_tot * w0;
+#pragma unroll
+  for (int sp = 0; sp < NKS - 1; ++sp) {
+    wsp[sp] = fast_exp2(part[(sp * NE + DB * 16) * 64 + lane] - M_use);
+    l_all = fmaf(part[(sp * NE + DB * 16 + 1) * 64 + lane], wsp[sp], l_all);
+  }
+  const float inv = 1.0f / fmaxf(l_all, 1e-30f);
   if (qi < L) {
     T* op = out + int64_t(seq0 + qi) * q_row + h * D;
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
       float r[16];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) r[j] = (o[db][j] * w0 + mine[(db * 16 + j) * 64 + lane] * w1) * inv;
+      for (int j = 0; j < 16; ++j) {
+        float acc = o[db][j] * w0;
+#pragma unroll
+        for (int sp = 0; sp < NKS - 1; ++sp) acc = fmaf(part[(sp * NE + db * 16 + j) * 64 + lane], wsp[sp], acc);
+        r[j] = acc * inv;
+      }
       // lane owns query qi and, per 32-wide D block, d = (j/4)*8 + 4g + (j%4): four runs
       // of 4 consecutive elements.
 #pragma unroll
@@ -418,14 +441,14 @@ __global__ __launch_bounds__(kThreads, D <= 128 ? 2 : 1) void varlen_prefill_ker
 
 int rows_per_tile() { return kBQ; }
 
-int keys_per_tile() { return kBK; }
+int keys_per_tile(int D) { return D <= 128 ? Tiles<128>::BK : Tiles<256>::BK; }
 
 template <typename T, int D>
 int launch2(const void* q, const void* k, const void* v, void* out, const int32_t* cu,
             const int32_t* sched, int n_tiles, int H, int H_kv, float scale_log2, int causal,
             hipStream_t s) {
   dim3 grid(H, n_tiles);
-  hipLaunchKernelGGL((varlen_prefill_kernel<T, D>), grid, dim3(kThreads), 0, s,
+  hipLaunchKernelGGL((varlen_prefill_kernel<T, D>), grid, dim3(Tiles<D>::THREADS), 0, s,
                      static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
                      static_cast<T*>(out), cu, sched, H, H_kv, H / H_kv, scale_log2, causal);
   return launch_status("mi_varlen_prefill");
@@ -459,9 +482,8 @@ extern "C" int mi_varlen_schedule(const int32_t* host_cu_seqlens, int n_seqs, in
     return fail(MI_ERR_INVALID, "mi_varlen_schedule: n_head (%d) must be a multiple of n_kv_head (%d)",
                 H, H_kv);
   }
-  (void)D;
   const int RW = rows_per_tile();
-  const int BN = keys_per_tile();
+  const int BN = keys_per_tile(D);
   struct Item { int work, seq, tile; };
   std::vector<Item> items;
   for (int s = 0; s < n_seqs; ++s) {

@@ -1,0 +1,256 @@
+"""Random-init Qwen3-0.6B driven through the MI355X attention path (the end-to-end harness).
+
+The model is the reference's ``MiniLLM`` at the Qwen3 shape (reference ``model/minillm.py``,
+``model/layers.py``): tied token embedding, 28 blocks of pre-norm attention + SwiGLU MLP,
+per-head q/k RMSNorm, NeoX RoPE with theta 1e6, RMSNorm computed in the activation dtype,
+bf16 weights drawn N(0, 0.02). Only the attention path is this package's: packed prefill
+goes through :class:`~miattn.packed.PackedPrefill` (HIP varlen kernel + one slot-write
+launch per layer) and decode through :class:`~miattn.paged.PagedKV` (HIP slot write +
+block-table decode), exactly the containers the reference's layers call
+(reference ``model/layers.py:217-250``). Projections, norms and RoPE are plain torch.
+
+:class:`GraphDecoder` is the decode step with no host work per step: slot map, seqlen,
+RoPE rows, 28 layers, lm_head and the greedy argmax are captured once in a HIP graph and
+replayed (the reference parks this, ``serve/graph.py:1-40``; the host-bound step it
+measures is ``serve/graph.py:9-10``).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+from .decode import paged_decode_plan
+from .packed import PackedPrefill
+from .paged import PagedKV, PagedPool, PagedWriteSink
+
+__all__ = ["Qwen3Config", "random_weights", "Qwen3", "GraphDecoder"]
+
+
+@dataclass(frozen=True)
+class Qwen3Config:
+    """Qwen3-0.6B (reference ``model/config.py`` fields, Qwen3 values)."""
+
+    vocab: int = 151936
+    hidden: int = 1024
+    inter: int = 3072
+    n_layer: int = 28
+    n_head: int = 16
+    n_kv_head: int = 8
+    head_dim: int = 128
+    eps: float = 1e-6
+    rope_theta: float = 1e6
+    std: float = 0.02
+
+
+def random_weights(cfg: Qwen3Config, seed: int, dtype=torch.bfloat16) -> dict:
+    """N(0, std) embedding and projections, unit norms (reference ``_init_weights``,
+    ``model/minillm.py:57-64``), drawn on the CPU in a fixed order so every host and test
+    sees the same values for a seed."""
+    gen = torch.Generator().manual_seed(seed)
+
+    def normal(*shape):
+        return (torch.randn(*shape, generator=gen) * cfg.std).to(dtype)
+
+    H, Hk, D, C = cfg.n_head, cfg.n_kv_head, cfg.head_dim, cfg.hidden
+    w = {"embed": normal(cfg.vocab, C), "norm": torch.ones(C, dtype=dtype)}
+    for i in range(cfg.n_layer):
+        p = f"l{i}."
+        w[p + "wq"] = normal(H * D, C)
+        w[p + "wk"] = normal(Hk * D, C)
+        w[p + "wv"] = normal(Hk * D, C)
+        w[p + "wo"] = normal(C, H * D)
+        w[p + "wg"] = normal(cfg.inter, C)
+        w[p + "wu"] = normal(cfg.inter, C)
+        w[p + "wd"] = normal(C, cfg.inter)
+        for n in ("ln1", "ln2"):
+            w[p + n] = torch.ones(C, dtype=dtype)
+        for n in ("qn", "kn"):
+            w[p + n] = torch.ones(D, dtype=dtype)
+    return w
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """``x / sqrt(mean(x^2) + eps) * weight`` in x's dtype (reference ``model/layers.py:342-350``)."""
+    rms = torch.sqrt(x.pow(2).mean(-1, True) + eps)
+    return x / rms * weight
+
+
+def rope_table(head_dim: int, theta: float, length: int, device, dtype):
+    """cos/sin ``(length, head_dim/2)`` in the model dtype (reference ``rope_cos_sin``)."""
+    inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float32, device=device) / head_dim))
+    angles = torch.outer(torch.arange(length, dtype=torch.float32, device=device), inv_freq)
+    return angles.cos().to(dtype), angles.sin().to(dtype)
+
+
+def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """NeoX halves rotation; ``cos``/``sin`` broadcast against ``x``'s ``(..., H, D)``
+    with a head axis inserted (reference ``apply_rotary_emb``)."""
+    half = x.shape[-1] // 2
+    x1, x2 = x[..., :half], x[..., half:]
+    cos, sin = cos.unsqueeze(-2), sin.unsqueeze(-2)
+    return torch.cat([x1 * cos - x2 * sin, x1 * sin + x2 * cos], dim=-1)
+
+
+class Qwen3:
+    """The model on one HIP device, attention through this package's containers."""
+
+    def __init__(self, cfg: Qwen3Config, weights: dict, device, *, max_pos: int = 8192) -> None:
+        _lib.require_library("the Qwen3 end-to-end harness")
+        self.cfg = cfg
+        self.device = torch.device(device)
+        self.w = {k: v.to(self.device) for k, v in weights.items()}
+        self.dtype = self.w["embed"].dtype
+        self.cos, self.sin = rope_table(cfg.head_dim, cfg.rope_theta, max_pos, self.device, self.dtype)
+
+    # ------------------------------------------------------------------ pieces
+    def _qkv(self, i: int, x: torch.Tensor):
+        c, p = self.cfg, f"l{i}."
+        lead = x.shape[:-1]
+        q = rms_norm(F.linear(x, self.w[p + "wq"]).view(*lead, c.n_head, c.head_dim), self.w[p + "qn"], c.eps)
+        k = rms_norm(F.linear(x, self.w[p + "wk"]).view(*lead, c.n_kv_head, c.head_dim), self.w[p + "kn"], c.eps)
+        v = F.linear(x, self.w[p + "wv"]).view(*lead, c.n_kv_head, c.head_dim)
+        return q, k, v
+
+    def _mlp(self, i: int, x: torch.Tensor) -> torch.Tensor:
+        p = f"l{i}."
+        return F.linear(F.silu(F.linear(x, self.w[p + "wg"])) * F.linear(x, self.w[p + "wu"]), self.w[p + "wd"])
+
+    def logits(self, x: torch.Tensor) -> torch.Tensor:
+        return F.linear(rms_norm(x, self.w["norm"], self.cfg.eps), self.w["embed"])
+
+    def new_pool(self, n_blocks: int, block_size: int = 16) -> PagedPool:
+        c = self.cfg
+        return PagedPool(c.n_layer, n_blocks, block_size, c.n_kv_head, c.head_dim, dtype=self.dtype,
+                         device=self.device, n_head=c.n_head)
+
+    # ------------------------------------------------------------------ prefill
+    def prefill(self, prompts: list[list[int]], pool: PagedPool, tables: list[list[int]]) -> torch.Tensor:
+        """Packed prefill of whole prompts (reference ``MiniLLM.forward`` packed branch,
+        ``model/minillm.py:76-106``); writes every layer's K/V into ``pool`` through the
+        requests' block tables and returns the last-token logits ``(n_prompts, vocab)``."""
+        c = self.cfg
+        lengths = [len(p) for p in prompts]
+        cu = [0]
+        for n in lengths:
+            cu.append(cu[-1] + n)
+        positions = torch.cat([torch.arange(n) for n in lengths]).to(self.device)
+        sinks = [PagedWriteSink(pool, t, n) for t, n in zip(tables, lengths)]
+        packed = PackedPrefill(cu_seqlens=cu, positions=positions, sinks=sinks)
+        tokens = torch.tensor([t for p in prompts for t in p], dtype=torch.long, device=self.device)
+        x = F.embedding(tokens, self.w["embed"]).unsqueeze(0)  # (1, T, C)
+        cos, sin = self.cos[positions], self.sin[positions]
+        for i in range(c.n_layer):
+            h = rms_norm(x, self.w[f"l{i}.ln1"], c.eps)
+            q, k, v = self._qkv(i, h)
+            q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
+            packed.write(i, k, v)
+            y = packed.attend(q, k, v)
+            x = x + F.linear(y.reshape(1, -1, c.n_head * c.head_dim), self.w[f"l{i}.wo"])
+            x = x + self._mlp(i, rms_norm(x, self.w[f"l{i}.ln2"], c.eps))
+        return self.logits(x[0, packed.last_token_index])
+
+    # ------------------------------------------------------------------ decode
+    def decode(self, paged: PagedKV, tokens: torch.Tensor) -> torch.Tensor:
+        """One decode step of every row (reference ``MiniLLM.forward`` decode-container
+        branch, ``model/minillm.py:111-136``); returns logits ``(B, vocab)``."""
+        c = self.cfg
+        paged.build_mask(next_token=True)
+        cos, sin = self.cos[paged.pos].unsqueeze(1), self.sin[paged.pos].unsqueeze(1)  # (B, 1, D/2)
+        x = F.embedding(tokens.view(-1, 1), self.w["embed"])  # (B, 1, C)
+        for i in range(c.n_layer):
+            h = rms_norm(x, self.w[f"l{i}.ln1"], c.eps)
+            q, k, v = self._qkv(i, h)  # (B, 1, H, D)
+            q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
+            paged.write(i, k.permute(0, 2, 1, 3), v.permute(0, 2, 1, 3))
+            y = paged.attend(i, q.transpose(1, 2))  # (B, H, 1, D)
+            x = x + F.linear(y.transpose(1, 2).reshape(x.shape[0], 1, -1), self.w[f"l{i}.wo"])
+            x = x + self._mlp(i, rms_norm(x, self.w[f"l{i}.ln2"], c.eps))
+        paged.advance()
+        return self.logits(x[:, 0])
+
+
+class GraphDecoder:
+    """Greedy decode steps of a fixed batch, each replayed from one captured HIP graph.
+
+    Device state per row: the next input token, its position, an int32 seqlen, and the
+    row's block table; every step computes the write slot ``table[pos // bs] * bs + pos % bs``
+    (reference ``model/paged.py:499-501``) and ``seqlen = pos + 1`` on the device, runs the
+    28 layers (HIP slot write + HIP paged decode per layer), takes the argmax and advances
+    ``pos``. ``history`` collects the generated tokens.
+    """
+
+    def __init__(self, model: Qwen3, pool: PagedPool, tables: list[list[int]], lengths: list[int],
+                 first_tokens: torch.Tensor, max_new: int) -> None:
+        c = model.cfg
+        dev = model.device
+        self.model, self.pool = model, pool
+        B = len(tables)
+        max_blocks = max(len(t) for t in tables)
+        for t, n in zip(tables, lengths):
+            if (n + max_new + pool.block_size - 1) // pool.block_size > len(t):
+                raise ValueError(f"block table of {len(t)} blocks cannot hold {n} + {max_new} tokens")
+        bt = torch.zeros(B, max_blocks, dtype=torch.int32)
+        for r, t in enumerate(tables):
+            bt[r, : len(t)] = torch.tensor(t, dtype=torch.int32)
+        self.table = bt.to(dev)
+        self.table64 = self.table.to(torch.int64)
+        self.pos = torch.tensor(lengths, dtype=torch.long, device=dev)
+        self.seqlen = (self.pos + 1).to(torch.int32)
+        self.tokens = first_tokens.to(dev, torch.long).clone()
+        self.history = torch.zeros(B, max_new, dtype=torch.long, device=dev)
+        self.step_idx = torch.zeros(1, dtype=torch.long, device=dev)
+        self.max_new = max_new
+        self.B = B
+        q0 = torch.zeros(B, c.n_head, c.head_dim, dtype=model.dtype, device=dev)
+        self.plan = paged_decode_plan(q0, pool.keys, pool.values, self.table, self.seqlen,
+                                      scale=1.0 / math.sqrt(c.head_dim))
+        self.graph = None
+
+    def _step(self) -> None:
+        m, c, bs = self.model, self.model.cfg, self.pool.block_size
+        self.seqlen.copy_((self.pos + 1).to(torch.int32))
+        slots = self.table64.gather(1, (self.pos // bs).view(-1, 1)).view(-1) * bs + self.pos % bs
+        cos, sin = m.cos[self.pos].unsqueeze(1), m.sin[self.pos].unsqueeze(1)
+        x = F.embedding(self.tokens.view(-1, 1), m.w["embed"])
+        for i in range(c.n_layer):
+            h = rms_norm(x, m.w[f"l{i}.ln1"], c.eps)
+            q, k, v = m._qkv(i, h)
+            q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
+            self.pool.write_slots(i, slots, k[:, 0], v[:, 0])
+            y = self.plan.run(i, q[:, 0].contiguous())  # (B, H, D)
+            x = x + F.linear(y.reshape(self.B, 1, -1), m.w[f"l{i}.wo"])
+            x = x + m._mlp(i, rms_norm(x, m.w[f"l{i}.ln2"], c.eps))
+        nxt = m.logits(x[:, 0]).argmax(-1)
+        self.history.index_copy_(1, self.step_idx, nxt.view(-1, 1))
+        self.tokens.copy_(nxt)
+        self.pos.add_(1)
+        self.step_idx.add_(1)
+
+    def capture(self, stream=None) -> None:
+        """Record one step (run once eagerly first so lazily built state exists) and undo
+        that warm-up step's effects on positions, history and the step counter."""
+        saved = (self.pos.clone(), self.tokens.clone())
+        self._step()
+        torch.cuda.synchronize()
+        self.pos.copy_(saved[0])
+        self.tokens.copy_(saved[1])
+        self.step_idx.zero_()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph, stream=stream):
+            self._step()
+        # capture recorded but did not run the step: restore the pre-step state
+        self.pos.copy_(saved[0])
+        self.tokens.copy_(saved[1])
+        self.step_idx.zero_()
+        torch.cuda.synchronize()
+
+    def step(self) -> None:
+        if self.graph is None:
+            self._step()
+        else:
+            self.graph.replay()

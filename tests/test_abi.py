@@ -62,7 +62,7 @@ def test_schedule_covers_every_tile_once_heaviest_first():
     expected = {(s, t) for s, n in enumerate(lengths) for t in range(-(-n // rows))}
     assert sorted(sched) == sorted(expected)
     work = [min(lengths[s], (t + 1) * rows) for s, t in sched]
-    kt = [-(-w // 64) for w in work]
+    kt = [-(-w // 64) for w in work]  # 64-key tiles
     assert kt == sorted(kt, reverse=True)
 
 
