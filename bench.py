@@ -283,6 +283,20 @@ def bench_tpot(stream, prompt_len: int = 1920, new_tokens: int = 128, B: int = 3
     }
 
 
+def profiled_traffic() -> float | None:
+    """HBM bytes per layer (split + merge launch) from the committed PMC summary
+    (``profiles/paged_decode_config2_counters.json``): FETCH_SIZE and WRITE_SIZE per
+    dispatch, each scaled by what the counter reads for a plain 1 GiB device copy."""
+    path = ROOT / "profiles" / "paged_decode_config2_counters.json"
+    try:
+        c = json.loads(path.read_text())
+    except (OSError, ValueError):
+        return None
+    fetch = c["fetch_kib_per_dispatch"] * (1048576.0 / c["copy_fetch_kib_for_1gib"])
+    write = c["write_kib_per_dispatch"] * (1048576.0 / c["copy_write_kib_for_1gib"])
+    return (fetch + write) * 1024.0
+
+
 def copy_calibration(mib: int, reps: int) -> dict:
     """A plain device copy of a known size, run under the same PMC counters as the decode
     kernel: FETCH_SIZE / WRITE_SIZE of this launch over its known bytes is the counters'
@@ -448,7 +462,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(dec["bytes_per_layer"] / (dec["us_per_layer"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": profiled_traffic(),
             "algorithmic_bytes_per_launch": dec["bytes_per_layer"],
         },
         "tpot_ms": None,

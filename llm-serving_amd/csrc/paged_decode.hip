@@ -30,7 +30,10 @@
 //     (m, l, acc) partial to the workspace and a second, small launch folds the partials
 //     with a log-sum-exp merge. (An in-kernel "last split merges" counter needs an
 //     agent-scope release per workgroup, which on the multi-XCD gfx950 writes back the
-//     XCD's L2 each time; measured several times slower than the extra launch.)
+//     XCD's L2 each time; measured 3x slower than the extra launch on config 2 even with
+//     a release-only fence, 122 vs 39 us per layer.)
+//   * K/V are read with the nontemporal hint: each byte is used once, and keeping it out
+//     of L2 lifted config 2 from 43.0 to 39.4 us and config 4 from 5.3 to 6.0 TB/s.
 // HBM-bound: per (token, KV head) the kernel reads 2 * D * esize bytes of K+V.
 #include "common.h"
 
@@ -71,6 +74,22 @@ struct Layout {
   static constexpr int U = unroll_for(GB);
   static_assert(LPR >= 1 && LPR <= 64 && (64 % LPR) == 0, "unsupported D/dtype");
 };
+
+// K/V are streamed once per launch: optionally read with the nontemporal hint so they do
+// not displace the block tables, q and partials in L2.
+#ifndef MIATTN_DECODE_NT
+#define MIATTN_DECODE_NT 1
+#endif
+template <typename P>
+__device__ __forceinline__ uint4 load_kv(const P* p) {
+  if constexpr (MIATTN_DECODE_NT) {
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+  } else {
+    return load16(p);
+  }
+}
 
 __device__ __forceinline__ int clamp_len(int len, int capacity) {
   len = len < capacity ? len : capacity;  // page-walk clamp (reference :593)
@@ -202,12 +221,12 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int off = token(t0, u) & bs_mask;
-      kr[u] = load16(kbase + int64_t(pg[u]) * a.ks0 + off * a.ks1);
+      kr[u] = load_kv(kbase + int64_t(pg[u]) * a.ks0 + off * a.ks1);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int off = token(t0, u) & bs_mask;
-      vr[u] = load16(vbase + int64_t(pg[u]) * a.vs0 + off * a.vs1);
+      vr[u] = load_kv(vbase + int64_t(pg[u]) * a.vs0 + off * a.vs1);
     }
   };
 
@@ -304,7 +323,6 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(
   __syncthreads();
 
   const int n_out = KVB * GB * D;
-  const int64_t slot = first_slot + split;
   for (int i = tid; i < n_out; i += kThreads) {
     const int kl = i / (GB * D), g = (i / D) % GB, d = i % D;
     float M = -INFINITY;
@@ -321,7 +339,8 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(
     if (n_split_b <= 1) {
       out[b * a.os0 + h * a.os1 + d] = from_f32<T>(As / fmaxf(Ls, 1.0f));
     } else {
-      const int64_t ph = slot * a.H + h;
+      // [head][slot]: the partials of one (row, head) are contiguous for the merge
+      const int64_t ph = int64_t(h) * a.slots + first_slot + split;
       ws_acc[ph * D + d] = As;
       if (d == 0) {
         ws_ml[ph * 2 + 0] = M;
@@ -331,61 +350,60 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(
   }
 }
 
-// Second launch, one workgroup per (query head, row): zero-length rows get exact zeros;
-// rows split over several workgroups get the log-sum-exp merge of their partials (the
-// (m, l) pairs are read in parallel, so the only serial part is the weighted sum over
-// splits); single-split rows were finished by the first launch.
+// Second launch, one workgroup per (query head, row), one thread per element of D:
+// zero-length rows get exact zeros; rows split over several workgroups get the
+// log-sum-exp merge of their partials, folded online (running max) 16 splits at a time
+// with every load of a chunk in flight together -- no LDS, no barrier: one round trip for
+// the row's (first slot, split count) record written by the first launch, then one per 16
+// splits. Single-split rows were finished by the first launch.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void paged_decode_merge_kernel(
     const int32_t* __restrict__ seqlen, const int32_t* __restrict__ ws_rows,
     const float* __restrict__ ws_ml, const float* __restrict__ ws_acc, T* __restrict__ out,
     DecodeArgs a) {
-  extern __shared__ float sw[];  // [n] weights
-  __shared__ float s_red[4];
+  constexpr int kChunk = 16;
   const int h = blockIdx.x;
   const int b = blockIdx.y;
-  const int tid = threadIdx.x;
+  const int d = threadIdx.x;
   const int capacity = a.max_blocks << a.bs_log2;
   const int len = clamp_len(seqlen[b], capacity);
+  const int first = ws_rows[2 * b];      // read before the branch: both loads in flight
+  const int n_split = ws_rows[2 * b + 1];
+  if (d >= D) return;
   T* orow = out + b * a.os0 + h * a.os1;
   if (len == 0) {
-    for (int d = tid; d < D; d += blockDim.x) orow[d] = from_f32<T>(0.0f);
+    orow[d] = from_f32<T>(0.0f);
     return;
   }
-  // Split 0 of every non-empty row recorded where the row's partials start and how many
-  // there are; a row the first launch finished in place (one split) needs nothing here.
-  const int first = ws_rows[2 * b];
-  const int n_split = ws_rows[2 * b + 1];
   if (n_split <= 1) return;
-  const int64_t base = int64_t(first) * a.H + h;
-  float mloc = -INFINITY;
-  for (int s = tid; s < n_split; s += blockDim.x) mloc = fmaxf(mloc, ws_ml[(base + int64_t(s) * a.H) * 2]);
-  mloc = group_allreduce<64, MaxOp>(mloc);
-  if ((tid & 63) == 0) s_red[tid >> 6] = mloc;
-  __syncthreads();
-  float M = s_red[0];
-  for (int wv = 1; wv < int(blockDim.x >> 6); ++wv) M = fmaxf(M, s_red[wv]);
-  const float M_use = M == -INFINITY ? 0.0f : M;
-  float lloc = 0.0f;
-  for (int s = tid; s < n_split; s += blockDim.x) {
-    const int64_t ph = base + int64_t(s) * a.H;
-    const float wgt = fast_exp2(ws_ml[ph * 2] - M_use);
-    sw[s] = wgt;
-    lloc = fmaf(ws_ml[ph * 2 + 1], wgt, lloc);
+  const float* ml = ws_ml + (int64_t(h) * a.slots + first) * 2;  // [head][slot] layout
+  const float* acc = ws_acc + (int64_t(h) * a.slots + first) * D + d;
+  float M = -INFINITY, Ls = 0.0f, As = 0.0f;
+  for (int s0 = 0; s0 < n_split; s0 += kChunk) {
+    float m[kChunk], l[kChunk], v[kChunk];
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) {
+      const int sp = min(s0 + j, n_split - 1);  // repeated tail entries are weighted out below
+      m[j] = ml[sp * 2];
+      l[j] = ml[sp * 2 + 1];
+      v[j] = acc[int64_t(sp) * D];
+    }
+    float Mc = M;
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) Mc = s0 + j < n_split ? fmaxf(Mc, m[j]) : Mc;
+    const float Mu = Mc == -INFINITY ? 0.0f : Mc;
+    const float r = fast_exp2(M - Mu);
+    Ls *= r;
+    As *= r;
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) {
+      const float w = s0 + j < n_split ? fast_exp2(m[j] - Mu) : 0.0f;
+      Ls = fmaf(l[j], w, Ls);
+      As = fmaf(v[j], w, As);
+    }
+    M = Mc;
   }
-  lloc = group_allreduce<64, SumOp>(lloc);
-  __syncthreads();
-  if ((tid & 63) == 0) s_red[tid >> 6] = lloc;
-  __syncthreads();
-  float Ls = 0.0f;
-  for (int wv = 0; wv < int(blockDim.x >> 6); ++wv) Ls += s_red[wv];
-  const float inv = 1.0f / fmaxf(Ls, 1.0f);
-  for (int d = tid; d < D; d += blockDim.x) {
-    float As = 0.0f;
-#pragma unroll 8
-    for (int s = 0; s < n_split; ++s) As = fmaf(ws_acc[(base + int64_t(s) * a.H) * D + d], sw[s], As);
-    orow[d] = from_f32<T>(As * inv);
-  }
+  orow[d] = from_f32<T>(As / fmaxf(Ls, 1.0f));
 }
 
 int ilog2_exact(int x) {
@@ -407,7 +425,7 @@ struct Plan {
   size_t smem_bytes;
 };
 
-Plan make_plan(int B, int H, int H_kv, int D, int dtype) {
+Plan make_plan(int B, int H, int H_kv, int D, int block_size, int max_blocks, int dtype) {
   Plan p{};
   const int es = esize_of(dtype);
   const int lpr = D * es / 16;
@@ -453,9 +471,8 @@ int launch_typed(const void* q, const void* kc, const void* vc, const int32_t* b
   int rc = launch_status("mi_paged_decode (split kernel)");
   if (rc != MI_OK) return rc;
   const int threads = D > 64 ? D : 64;
-  hipLaunchKernelGGL((paged_decode_merge_kernel<T, D>), dim3(a.H, a.B), dim3(threads),
-                     size_t(p.slots) * sizeof(float), stream, seqlen, ws_rows, ws_ml, ws_acc,
-                     static_cast<T*>(out), a);
+  hipLaunchKernelGGL((paged_decode_merge_kernel<T, D>), dim3(a.H, a.B), dim3(threads), 0, stream,
+                     seqlen, ws_rows, ws_ml, ws_acc, static_cast<T*>(out), a);
   return launch_status("mi_paged_decode (merge kernel)");
 }
 
@@ -503,7 +520,7 @@ extern "C" size_t mi_paged_decode_workspace_size(int B, int H, int H_kv, int D, 
                                                  int max_blocks, int dtype) {
   using namespace miattn;
   if (!shape_ok(B, H, H_kv, D, block_size, max_blocks, dtype)) return 0;
-  const Plan p = make_plan(B, H, H_kv, D, dtype);
+  const Plan p = make_plan(B, H, H_kv, D, block_size, max_blocks, dtype);
   return p.rows_bytes + p.ml_bytes + p.acc_bytes;
 }
 
@@ -552,7 +569,7 @@ extern "C" int mi_paged_decode(const void* q, const void* k_cache, const void* v
                 (long long)st[0], (long long)st[1], (long long)st[2], (long long)st[3],
                 (long long)st[4], (long long)st[5], (long long)st[6]);
   }
-  const Plan p = make_plan(B, H, H_kv, D, dtype);
+  const Plan p = make_plan(B, H, H_kv, D, block_size, max_blocks, dtype);
   if (p.n_groups * p.n_hchunks > 65535 || B > 65535 || H > 65535) {
     return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode: grid too large (B=%d, H=%d)", B, H);
   }
