@@ -126,7 +126,12 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* s_tmp, int& tota
   return before + inc - v;
 }
 
-template <typename T, int D, int GB>
+// UP ("uniform pages"): every lane of a wave reads the same token of a workgroup-wide load
+// (rows per wave <= KV heads per group, true at the Qwen3 shape), so the block-table
+// entries are wave-uniform and read with scalar loads. Those are counted apart from the
+// K/V vector loads, so the in-order vector-load counter tracks only K/V batches and the
+// reduction of batch i never waits for batch i+1.
+template <typename T, int D, int GB, bool UP>
 __global__ __launch_bounds__(kThreads) void paged_decode_kernel(
     const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc,
     const int32_t* __restrict__ block_table, const int32_t* __restrict__ seqlen,
@@ -214,8 +219,18 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(
     return tok < t_end ? tok : t_begin;
   };
   auto load_pages = [&](int t0, int (&pg)[U]) {
+    if constexpr (UP) {
+      const int ts = __builtin_amdgcn_readfirstlane(tsub);
 #pragma unroll
-    for (int u = 0; u < U; ++u) pg[u] = bt_row[token(t0, u) >> a.bs_log2];
+      for (int u = 0; u < U; ++u) {
+        int tok = t0 + u * TPL + ts;
+        tok = tok < t_end ? tok : t_begin;
+        pg[u] = bt_row[tok >> a.bs_log2];
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < U; ++u) pg[u] = bt_row[token(t0, u) >> a.bs_log2];
+    }
   };
   auto issue = [&](int t0, const int (&pg)[U], uint4 (&kr)[U], uint4 (&vr)[U]) {
 #pragma unroll
@@ -228,10 +243,10 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(
       const int off = token(t0, u) & bs_mask;
       vr[u] = load_kv(vbase + int64_t(pg[u]) * a.vs0 + off * a.vs1);
     }
+    // keep each batch's loads together and in program order (see the pipeline below)
+    __builtin_amdgcn_sched_barrier(0);
   };
 
-  int pg_next[U], pg_after[U];
-  load_pages(t_begin, pg_next);
   float qv[GB][EPL];
 #pragma unroll
   for (int g = 0; g < GB; ++g) {
@@ -249,21 +264,9 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(
     for (int e = 0; e < EPL; ++e) acc[g][e] = 0.0f;
   }
 
-  uint4 kr[U], vr[U];
-  if (t_begin + batch < t_end) load_pages(t_begin + batch, pg_after);
-  issue(t_begin, pg_next, kr, vr);
-  for (int t0 = t_begin; t0 < t_end; t0 += batch) {
-    // issue order per iteration: pages two batches ahead, then K/V one batch ahead, so
-    // the in-order load counter never makes the K/V issue wait for this batch's data
-    uint4 kn[U], vn[U];
-    const bool more = t0 + batch < t_end;
-    if (more) {
-#pragma unroll
-      for (int u = 0; u < U; ++u) pg_next[u] = pg_after[u];
-      if (t0 + 2 * batch < t_end) load_pages(t0 + 2 * batch, pg_after);
-      issue(t0 + batch, pg_next, kn, vn);
-    }
-
+  // Online softmax over one batch of U tokens per row state.
+  auto compute = [&](int t0, const uint4 (&kr)[U], const uint4 (&vr)[U]) {
+    __builtin_amdgcn_sched_barrier(0);
     float s[U][GB];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -298,14 +301,38 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(
       }
       l[g] = lsum_g;
     }
-    if (more) {
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        kr[u] = kn[u];
-        vr[u] = vn[u];
-      }
-    }
+  };
+
+  // Software pipeline with two statically named register sets (A, B) and the loop
+  // unrolled by two: while batch i is reduced, batch i+1 is in flight, and the block-table
+  // entries of the batch after are loaded one step ahead of its K/V. Inside the loop every
+  // issue is unconditional (the bound guarantees the batch exists), so the compiler can
+  // wait for exactly the batch being reduced; a copy between sets or a conditional issue
+  // makes it wait for all loads in flight. Loads past t_end are harmless: token() clamps
+  // them to t_begin, a valid token of this split (the plan gives no workgroup an empty
+  // range), and compute() masks them out.
+  const int n_b = (t_end - t_begin + batch - 1) / batch;
+  int pgA[U], pgB[U];
+  uint4 kA[U], vA[U], kB[U], vB[U];
+  load_pages(t_begin, pgA);
+  load_pages(t_begin + batch, pgB);
+  issue(t_begin, pgA, kA, vA);
+  issue(t_begin + batch, pgB, kB, vB);  // unconditional (see above); n_b >= 1 always
+  load_pages(t_begin + 2 * batch, pgA);
+  int i = 0;
+  for (; i + 2 < n_b; i += 2) {
+    const int t0 = t_begin + i * batch;
+    compute(t0, kA, vA);
+    load_pages(t0 + 3 * batch, pgB);
+    issue(t0 + 2 * batch, pgA, kA, vA);
+    compute(t0 + batch, kB, vB);
+    load_pages(t0 + 4 * batch, pgA);
+    issue(t0 + 3 * batch, pgB, kB, vB);
   }
+  // One or two batches left: A holds batch i, B batch i+1 (past n_b B's loads were
+  // clamped and are dropped). No issue is conditional, so nothing gets sunk into a branch.
+  compute(t_begin + i * batch, kA, vA);
+  if (n_b - i == 2) compute(t_begin + (i + 1) * batch, kB, vB);
 
   // Merge the TPL row states of each KV head through LDS.
   float* sm_m = smem;
@@ -464,10 +491,17 @@ int launch_typed(const void* q, const void* kc, const void* vc, const int32_t* b
     return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode: internal launch-geometry mismatch");
   }
   dim3 grid(p.slots, p.n_groups * p.n_hchunks);
-  hipLaunchKernelGGL((paged_decode_kernel<T, D, GB>), grid, dim3(kThreads), p.smem_bytes, stream,
-                     static_cast<const T*>(q), static_cast<const T*>(kc),
-                     static_cast<const T*>(vc), bt, seqlen, static_cast<T*>(out), ws_rows, ws_ml,
-                     ws_acc, a);
+  if (Layout<T, D, GB>::RPW <= p.KVB) {
+    hipLaunchKernelGGL((paged_decode_kernel<T, D, GB, true>), grid, dim3(kThreads), p.smem_bytes,
+                       stream, static_cast<const T*>(q), static_cast<const T*>(kc),
+                       static_cast<const T*>(vc), bt, seqlen, static_cast<T*>(out), ws_rows, ws_ml,
+                       ws_acc, a);
+  } else {
+    hipLaunchKernelGGL((paged_decode_kernel<T, D, GB, false>), grid, dim3(kThreads), p.smem_bytes,
+                       stream, static_cast<const T*>(q), static_cast<const T*>(kc),
+                       static_cast<const T*>(vc), bt, seqlen, static_cast<T*>(out), ws_rows, ws_ml,
+                       ws_acc, a);
+  }
   int rc = launch_status("mi_paged_decode (split kernel)");
   if (rc != MI_OK) return rc;
   const int threads = D > 64 ? D : 64;
