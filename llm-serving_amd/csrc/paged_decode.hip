@@ -35,6 +35,8 @@
 //   * K/V are read with the nontemporal hint: each byte is used once, and keeping it out
 //     of L2 lifted config 2 from 43.0 to 39.4 us and config 4 from 5.3 to 6.0 TB/s.
 // HBM-bound: per (token, KV head) the kernel reads 2 * D * esize bytes of K+V.
+#include <type_traits>
+
 #include "common.h"
 
 namespace miattn {
@@ -49,11 +51,16 @@ struct DecodeArgs {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 
-// Splits a launch aims for: 2 per CU of the 256-CU MI355X, all resident at once.
+// Workgroups a launch aims for: 2 per CU of the 256-CU MI355X, all resident at once.
 #ifndef MIATTN_DECODE_TARGET_SPLITS
 #define MIATTN_DECODE_TARGET_SPLITS 512
 #endif
 constexpr int kTargetSplits = MIATTN_DECODE_TARGET_SPLITS;
+
+// Upper bound on the KV heads one workgroup streams side by side.
+#ifndef MIATTN_DECODE_KVB_MAX
+#define MIATTN_DECODE_KVB_MAX 64
+#endif
 
 // Tokens per row state per batch, by query heads per lane: the next batch's K/V
 // registers (2 * U * 16 B per lane) are live while the current batch is reduced.
@@ -91,39 +98,110 @@ __device__ __forceinline__ uint4 load_kv(const P* p) {
   }
 }
 
+// q.k over one lane's 16-byte slices of q and k, accumulated onto `acc` in order. 16-bit
+// types use the packed dot2 instructions (v_dot2c_f32_bf16 / v_dot2c_f32_f16: two
+// products of 16-bit inputs, exact in fp32, added in fp32), so k is never unpacked.
+template <typename T>
+__device__ __forceinline__ float dot16(const uint4& q, const uint4& k, float acc);
+template <>
+__device__ __forceinline__ float dot16<bf16_t>(const uint4& q, const uint4& k, float acc) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, q.x), __builtin_bit_cast(bf16x2, k.x), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, q.y), __builtin_bit_cast(bf16x2, k.y), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, q.z), __builtin_bit_cast(bf16x2, k.z), acc, false);
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, q.w), __builtin_bit_cast(bf16x2, k.w), acc, false);
+}
+template <>
+__device__ __forceinline__ float dot16<f16_t>(const uint4& q, const uint4& k, float acc) {
+  typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+  acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, q.x), __builtin_bit_cast(f16x2, k.x), acc, false);
+  acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, q.y), __builtin_bit_cast(f16x2, k.y), acc, false);
+  acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, q.z), __builtin_bit_cast(f16x2, k.z), acc, false);
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, q.w), __builtin_bit_cast(f16x2, k.w), acc, false);
+}
+template <>
+__device__ __forceinline__ float dot16<float>(const uint4& q, const uint4& k, float acc) {
+  acc = fmaf(__uint_as_float(q.x), __uint_as_float(k.x), acc);
+  acc = fmaf(__uint_as_float(q.y), __uint_as_float(k.y), acc);
+  acc = fmaf(__uint_as_float(q.z), __uint_as_float(k.z), acc);
+  return fmaf(__uint_as_float(q.w), __uint_as_float(k.w), acc);
+}
+
+// EPL fp32 values -> one 16-byte vector of T (round-to-nearest-even for 16-bit types).
+template <typename T>
+__device__ __forceinline__ uint4 pack16(const float* v) {
+  if constexpr (sizeof(T) == 4) {
+    return make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                      __float_as_uint(v[3]));
+  } else {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      w[i] = uint32_t(from_f32<T>(v[2 * i]).bits) | (uint32_t(from_f32<T>(v[2 * i + 1]).bits) << 16);
+    }
+    return make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
 __device__ __forceinline__ int clamp_len(int len, int capacity) {
   len = len < capacity ? len : capacity;  // page-walk clamp (reference :593)
   return len > 0 ? len : 0;
 }
 
 // Tokens per split for a batch holding `total` tokens (identical in both launches).
-__device__ __forceinline__ int split_chunk(int total, int batch) {
-  int chunk = (total + kTargetSplits - 1) / kTargetSplits;
+__device__ __forceinline__ int split_chunk(int total, int batch, int target) {
+  int chunk = (total + target - 1) / target;
   chunk = (chunk + batch - 1) / batch * batch;
   return chunk > batch ? chunk : batch;
 }
 
-// Exclusive prefix sum over the workgroup; `total` receives the sum of all threads.
-__device__ __forceinline__ int block_exclusive_scan(int v, int* s_tmp, int& total) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int inc = v;
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+  const int lane = __lane_id();
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
-    const int up = __shfl_up(inc, off, 64);
-    if (lane >= off) inc += up;
+    const int up = __shfl_up(v, off, 64);
+    if (lane >= off) v += up;
   }
-  if (lane == 63) s_tmp[wave] = inc;
-  __syncthreads();
-  int before = 0;
-  total = 0;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    const int t = s_tmp[w];
-    before += w < wave ? t : 0;
-    total += t;
+  return v;
+}
+
+// This workgroup's piece of the token-balanced split: row b, split index within the row,
+// the row's split count and the global index of its first split. Every wave derives it on
+// its own from the row lengths (same inputs, same answer), so planning needs no LDS and no
+// barrier; rows are taken 64 at a time, one per lane.
+struct SplitInfo {
+  int b, split, n_split, first, chunk;
+};
+__device__ __forceinline__ bool plan_split(const int32_t* __restrict__ seqlen, int B, int capacity,
+                                           int batch, int target, int w, SplitInfo& si) {
+  const int lane = __lane_id();
+  int total = 0;
+  for (int r0 = 0; r0 < B; r0 += 64) {
+    const int row = r0 + lane;
+    const int len = row < B ? clamp_len(seqlen[row], capacity) : 0;
+    total += __builtin_amdgcn_readlane(wave_inclusive_scan(len), 63);
   }
-  __syncthreads();
-  return before + inc - v;
+  const int chunk = split_chunk(total, batch, target);
+  int base = 0;  // splits of the rows before this block of 64
+  for (int r0 = 0; r0 < B; r0 += 64) {
+    const int row = r0 + lane;
+    const int n = row < B ? (clamp_len(seqlen[row], capacity) + chunk - 1) / chunk : 0;
+    const int incl = wave_inclusive_scan(n);
+    const uint64_t owner = __ballot(w >= base + incl - n && w < base + incl);
+    if (owner != 0) {
+      const int o = __ffsll(static_cast<unsigned long long>(owner)) - 1;
+      const int excl = __builtin_amdgcn_readlane(incl - n, o);
+      si.b = r0 + o;
+      si.split = w - base - excl;
+      si.n_split = __builtin_amdgcn_readlane(n, o);
+      si.first = base + excl;
+      si.chunk = chunk;
+      return true;
+    }
+    base += __builtin_amdgcn_readlane(incl, 63);
+  }
+  return false;  // w is past the last split
 }
 
 // UP ("uniform pages"): every lane of a wave reads the same token of a workgroup-wide load
@@ -139,9 +217,7 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(
     float* __restrict__ ws_acc, DecodeArgs a) {
   using Lay = Layout<T, D, GB>;
   constexpr int EPL = Lay::EPL, LPR = Lay::LPR, RPW = Lay::RPW, NR = Lay::NR, U = Lay::U;
-  extern __shared__ float smem[];  // [NR][GB] m, [NR][GB] l, [NR][GB][D] acc
-  __shared__ int s_tmp[kWaves];
-  __shared__ int s_info[4];
+  extern __shared__ float smem[];  // parked row states: [TPL-1][KVB][GB] (m, l), then acc
 
   const int tid = threadIdx.x;
   const int KVB = 1 << a.kvb_log2;
@@ -150,43 +226,10 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(
   const int capacity = a.max_blocks << a.bs_log2;
 
   // ---- device-side split plan: total tokens -> chunk -> this workgroup's (row, split)
-  const int per = (a.B + kThreads - 1) / kThreads;  // rows per thread
-  const int rbeg = tid * per;
-  int lsum = 0;
-  for (int i = 0; i < per; ++i) {
-    const int row = rbeg + i;
-    if (row < a.B) lsum += clamp_len(seqlen[row], capacity);
-  }
-  int total_tokens;
-  (void)block_exclusive_scan(lsum, s_tmp, total_tokens);
-  const int chunk = split_chunk(total_tokens, batch);
-  int nsum = 0;
-  for (int i = 0; i < per; ++i) {
-    const int row = rbeg + i;
-    if (row < a.B) nsum += (clamp_len(seqlen[row], capacity) + chunk - 1) / chunk;
-  }
-  int n_total;
-  const int excl = block_exclusive_scan(nsum, s_tmp, n_total);
-  const int w = blockIdx.x;
-  if (w >= n_total) return;  // uniform over the workgroup
-  if (w >= excl && w < excl + nsum) {  // exactly one thread owns w's row
-    int p = excl;
-    for (int i = 0; i < per; ++i) {
-      const int row = rbeg + i;
-      if (row >= a.B) break;
-      const int n_r = (clamp_len(seqlen[row], capacity) + chunk - 1) / chunk;
-      if (w < p + n_r) {
-        s_info[0] = row;
-        s_info[1] = w - p;
-        s_info[2] = n_r;
-        s_info[3] = p;
-        break;
-      }
-      p += n_r;
-    }
-  }
-  __syncthreads();
-  const int b = s_info[0], split = s_info[1], n_split_b = s_info[2], first_slot = s_info[3];
+  SplitInfo si;
+  if (!plan_split(seqlen, a.B, capacity, batch, a.target, blockIdx.x, si)) return;  // uniform
+  const int b = si.b, split = si.split, n_split_b = si.n_split, first_slot = si.first;
+  const int chunk = si.chunk;
   const int len = clamp_len(seqlen[b], capacity);
   const int t_begin = split * chunk;
   const int t_end = min(len, t_begin + chunk);
@@ -211,6 +254,11 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(
   const int bs_mask = (1 << a.bs_log2) - 1;
   const T* kbase = kc + kvh * a.ks2 + c * EPL;
   const T* vbase = vc + kvh * a.vs2 + c * EPL;
+  // UP: every lane of a wave reads the same token, so the page/token part of an address is
+  // wave-uniform (scalar registers) and each lane adds a constant 32-bit byte offset (the
+  // host checks it fits): the loads take the scalar-base form with no per-load VALU math.
+  const uint32_t klane = uint32_t((kvh * a.ks2 + c * EPL) * int64_t(sizeof(T)));
+  const uint32_t vlane = uint32_t((kvh * a.vs2 + c * EPL) * int64_t(sizeof(T)));
 
   // Token u of a batch starting at t0; past t_end it falls back to t_begin (always valid)
   // and is masked out of the softmax.
@@ -233,27 +281,41 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(
     }
   };
   auto issue = [&](int t0, const int (&pg)[U], uint4 (&kr)[U], uint4 (&vr)[U]) {
+    if constexpr (UP) {
+      const int ts = __builtin_amdgcn_readfirstlane(tsub);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int off = token(t0, u) & bs_mask;
-      kr[u] = load_kv(kbase + int64_t(pg[u]) * a.ks0 + off * a.ks1);
-    }
+      for (int u = 0; u < U; ++u) {
+        int tok = t0 + u * TPL + ts;
+        const int off = (tok < t_end ? tok : t_begin) & bs_mask;
+        const char* page = reinterpret_cast<const char*>(kc + (int64_t(pg[u]) * a.ks0 + off * a.ks1));
+        kr[u] = load_kv(page + klane);
+      }
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int off = token(t0, u) & bs_mask;
-      vr[u] = load_kv(vbase + int64_t(pg[u]) * a.vs0 + off * a.vs1);
+      for (int u = 0; u < U; ++u) {
+        int tok = t0 + u * TPL + ts;
+        const int off = (tok < t_end ? tok : t_begin) & bs_mask;
+        const char* page = reinterpret_cast<const char*>(vc + (int64_t(pg[u]) * a.vs0 + off * a.vs1));
+        vr[u] = load_kv(page + vlane);
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int off = token(t0, u) & bs_mask;
+        kr[u] = load_kv(kbase + int64_t(pg[u]) * a.ks0 + off * a.ks1);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int off = token(t0, u) & bs_mask;
+        vr[u] = load_kv(vbase + int64_t(pg[u]) * a.vs0 + off * a.vs1);
+      }
     }
     // keep each batch's loads together and in program order (see the pipeline below)
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  float qv[GB][EPL];
+  uint4 qr[GB];
 #pragma unroll
-  for (int g = 0; g < GB; ++g) {
-    const uint4 raw = load16(q + b * a.qs0 + (h0 + g) * a.qs1 + c * EPL);
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) qv[g][e] = Vec16<T>::get(raw, e);
-  }
+  for (int g = 0; g < GB; ++g) qr[g] = load16(q + b * a.qs0 + (h0 + g) * a.qs1 + c * EPL);
 
   float m[GB], l[GB], acc[GB][EPL];
 #pragma unroll
@@ -264,20 +326,21 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(
     for (int e = 0; e < EPL; ++e) acc[g][e] = 0.0f;
   }
 
-  // Online softmax over one batch of U tokens per row state.
-  auto compute = [&](int t0, const uint4 (&kr)[U], const uint4 (&vr)[U]) {
+  // Online softmax over one batch of U tokens per row state. Only a split's last batch
+  // can hold tokens past t_end, so the steady-state loop runs the unmasked form.
+  auto compute = [&](int t0, const uint4 (&kr)[U], const uint4 (&vr)[U], auto masked) {
     __builtin_amdgcn_sched_barrier(0);
     float s[U][GB];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const bool valid = t0 + u * TPL + tsub < t_end;
 #pragma unroll
       for (int g = 0; g < GB; ++g) {
-        float dot = 0.0f;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) dot = fmaf(qv[g][e], Vec16<T>::get(kr[u], e), dot);
+        float dot = dot16<T>(qr[g], kr[u], 0.0f);
         dot = group_allreduce<LPR, SumOp>(dot);
-        s[u][g] = valid ? dot * a.scale_log2 : -INFINITY;
+        s[u][g] = dot * a.scale_log2;
+        if constexpr (decltype(masked)::value) {
+          if (t0 + u * TPL + tsub >= t_end) s[u][g] = -INFINITY;
+        }
       }
     }
 #pragma unroll
@@ -322,57 +385,75 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(
   int i = 0;
   for (; i + 2 < n_b; i += 2) {
     const int t0 = t_begin + i * batch;
-    compute(t0, kA, vA);
+    compute(t0, kA, vA, std::false_type{});
     load_pages(t0 + 3 * batch, pgB);
     issue(t0 + 2 * batch, pgA, kA, vA);
-    compute(t0 + batch, kB, vB);
+    compute(t0 + batch, kB, vB, std::false_type{});
     load_pages(t0 + 4 * batch, pgA);
     issue(t0 + 3 * batch, pgB, kB, vB);
   }
   // One or two batches left: A holds batch i, B batch i+1 (past n_b B's loads were
   // clamped and are dropped). No issue is conditional, so nothing gets sunk into a branch.
-  compute(t_begin + i * batch, kA, vA);
-  if (n_b - i == 2) compute(t_begin + (i + 1) * batch, kB, vB);
+  compute(t_begin + i * batch, kA, vA, std::true_type{});
+  if (n_b - i == 2) compute(t_begin + (i + 1) * batch, kB, vB, std::true_type{});
 
-  // Merge the TPL row states of each KV head through LDS.
-  float* sm_m = smem;
-  float* sm_l = sm_m + NR * GB;
-  float* sm_acc = sm_l + NR * GB;
+  // Fold the TPL row states of each (KV head, query head, 16-byte slice) together: rows
+  // with tsub > 0 park theirs in LDS, rows with tsub == 0 merge them in registers and write
+  // whole 16-byte pieces of the output (or of the split's partial).
+  if (TPL > 1) {
+    float* sm_ml = smem;                             // [TPL-1][KVB][GB][2]
+    float* sm_acc = smem + (((TPL - 1) * KVB * GB * 2 + 3) & ~3);  // 16 B aligned: [TPL-1][KVB][GB][LPR][EPL]
+    if (tsub > 0) {
+#pragma unroll
+      for (int g = 0; g < GB; ++g) {
+        const int slot = ((tsub - 1) * KVB + kvl) * GB + g;
+        if (c == 0) *reinterpret_cast<float2*>(sm_ml + slot * 2) = make_float2(m[g], l[g]);
+        float4* dst = reinterpret_cast<float4*>(sm_acc + (slot * LPR + c) * EPL);
+#pragma unroll
+        for (int e = 0; e < EPL; e += 4) dst[e / 4] = make_float4(acc[g][e], acc[g][e + 1], acc[g][e + 2], acc[g][e + 3]);
+      }
+    }
+    __syncthreads();
+    if (tsub > 0) return;  // no barrier follows
+    for (int ts = 1; ts < TPL; ++ts) {
+#pragma unroll
+      for (int g = 0; g < GB; ++g) {
+        const int slot = ((ts - 1) * KVB + kvl) * GB + g;
+        const float2 ml2 = *reinterpret_cast<const float2*>(sm_ml + slot * 2);
+        const float M = fmaxf(m[g], ml2.x);
+        const float Mu = M == -INFINITY ? 0.0f : M;
+        const float w0 = fast_exp2(m[g] - Mu), w1 = fast_exp2(ml2.x - Mu);
+        m[g] = M;
+        l[g] = fmaf(l[g], w0, ml2.y * w1);
+        const float4* src = reinterpret_cast<const float4*>(sm_acc + (slot * LPR + c) * EPL);
+#pragma unroll
+        for (int e = 0; e < EPL; e += 4) {
+          const float4 o = src[e / 4];
+          acc[g][e + 0] = fmaf(acc[g][e + 0], w0, o.x * w1);
+          acc[g][e + 1] = fmaf(acc[g][e + 1], w0, o.y * w1);
+          acc[g][e + 2] = fmaf(acc[g][e + 2], w0, o.z * w1);
+          acc[g][e + 3] = fmaf(acc[g][e + 3], w0, o.w * w1);
+        }
+      }
+    }
+  }
+
 #pragma unroll
   for (int g = 0; g < GB; ++g) {
-    if (c == 0) {
-      sm_m[R * GB + g] = m[g];
-      sm_l[R * GB + g] = l[g];
-    }
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) sm_acc[(R * GB + g) * D + c * EPL + e] = acc[g][e];
-  }
-  __syncthreads();
-
-  const int n_out = KVB * GB * D;
-  for (int i = tid; i < n_out; i += kThreads) {
-    const int kl = i / (GB * D), g = (i / D) % GB, d = i % D;
-    float M = -INFINITY;
-    for (int ts = 0; ts < TPL; ++ts) M = fmaxf(M, sm_m[((ts << a.kvb_log2) + kl) * GB + g]);
-    const float M_use = M == -INFINITY ? 0.0f : M;
-    float Ls = 0.0f, As = 0.0f;
-    for (int ts = 0; ts < TPL; ++ts) {
-      const int Rs = (ts << a.kvb_log2) + kl;
-      const float wgt = fast_exp2(sm_m[Rs * GB + g] - M_use);
-      Ls = fmaf(sm_l[Rs * GB + g], wgt, Ls);
-      As = fmaf(sm_acc[(Rs * GB + g) * D + d], wgt, As);
-    }
-    const int h = (grp * KVB + kl) * a.G + hch * GB + g;
+    const int h = h0 + g;
     if (n_split_b <= 1) {
-      out[b * a.os0 + h * a.os1 + d] = from_f32<T>(As / fmaxf(Ls, 1.0f));
+      const float inv = 1.0f / fmaxf(l[g], 1.0f);
+      float o[EPL];
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) o[e] = acc[g][e] * inv;
+      store16(out + b * a.os0 + h * a.os1 + c * EPL, pack16<T>(o));
     } else {
       // [head][slot]: the partials of one (row, head) are contiguous for the merge
       const int64_t ph = int64_t(h) * a.slots + first_slot + split;
-      ws_acc[ph * D + d] = As;
-      if (d == 0) {
-        ws_ml[ph * 2 + 0] = M;
-        ws_ml[ph * 2 + 1] = Ls;
-      }
+      float4* dst = reinterpret_cast<float4*>(ws_acc + ph * D + c * EPL);
+#pragma unroll
+      for (int e = 0; e < EPL; e += 4) dst[e / 4] = make_float4(acc[g][e], acc[g][e + 1], acc[g][e + 2], acc[g][e + 3]);
+      if (c == 0) *reinterpret_cast<float2*>(ws_ml + ph * 2) = make_float2(m[g], l[g]);
     }
   }
 }
@@ -447,7 +528,7 @@ int lowbit(int x) { return x & -x; }
 
 // Launch geometry, computed identically by the workspace query and the launcher.
 struct Plan {
-  int GB, n_hchunks, KVB, kvb_log2, n_groups, NR, TPL, U, slots;
+  int GB, n_hchunks, KVB, kvb_log2, n_groups, NR, TPL, U, target, slots;
   size_t rows_bytes, ml_bytes, acc_bytes;
   size_t smem_bytes;
 };
@@ -469,16 +550,22 @@ Plan make_plan(int B, int H, int H_kv, int D, int block_size, int max_blocks, in
   }
   p.n_hchunks = G / p.GB;
   p.KVB = lowbit(H_kv) < p.NR ? lowbit(H_kv) : p.NR;
+  p.KVB = p.KVB < MIATTN_DECODE_KVB_MAX ? p.KVB : MIATTN_DECODE_KVB_MAX;
   p.kvb_log2 = ilog2_exact(p.KVB);
   p.n_groups = H_kv / p.KVB;
   p.TPL = p.NR / p.KVB;
   p.U = unroll_for(p.GB);
-  // Splits never exceed kTargetSplits + B: chunk >= total / kTargetSplits, and each row
-  // adds at most one partial split.
-  p.slots = kTargetSplits + B;
-  p.smem_bytes = size_t(p.NR) * p.GB * (D + 2) * sizeof(float);
+  // Each of the n_groups * n_hchunks workgroup columns splits the same token ranges, so
+  // the split target is shared out among them. Splits never exceed target + B: chunk >=
+  // total / target, and each row adds at most one partial split.
+  const int cols = p.n_groups * p.n_hchunks;
+  p.target = kTargetSplits / cols > 0 ? kTargetSplits / cols : 1;
+  p.slots = p.target + B;
+  // parked row states of the tsub > 0 rows: (m, l) pairs padded to 16 bytes, then acc
+  const size_t parked = size_t(p.TPL - 1) * p.KVB * p.GB;
+  p.smem_bytes = ((parked * 2 + 3) / 4 * 4 + parked * D) * sizeof(float);
   p.rows_bytes = (size_t(B) * 2 * sizeof(int32_t) + 255) / 256 * 256;
-  p.ml_bytes = size_t(p.slots) * H * 2 * sizeof(float);
+  p.ml_bytes = (size_t(p.slots) * H * 2 * sizeof(float) + 255) / 256 * 256;
   p.acc_bytes = size_t(p.slots) * H * D * sizeof(float);
   return p;
 }
@@ -491,7 +578,10 @@ int launch_typed(const void* q, const void* kc, const void* vc, const int32_t* b
     return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode: internal launch-geometry mismatch");
   }
   dim3 grid(p.slots, p.n_groups * p.n_hchunks);
-  if (Layout<T, D, GB>::RPW <= p.KVB) {
+  // Wave-uniform pages need every wave inside one token (RPW <= KVB) and the lane byte
+  // offsets within 32 bits.
+  const int64_t lane_span = (int64_t(a.H_kv) * std::max(a.ks2, a.vs2) + D) * int64_t(sizeof(T));
+  if (Layout<T, D, GB>::RPW <= p.KVB && a.ks2 >= 0 && a.vs2 >= 0 && lane_span < (int64_t(1) << 31)) {
     hipLaunchKernelGGL((paged_decode_kernel<T, D, GB, true>), grid, dim3(kThreads), p.smem_bytes,
                        stream, static_cast<const T*>(q), static_cast<const T*>(kc),
                        static_cast<const T*>(vc), bt, seqlen, static_cast<T*>(out), ws_rows, ws_ml,
@@ -595,10 +685,11 @@ extern "C" int mi_paged_decode(const void* q, const void* k_cache, const void* v
   const bool strides_ok = (st[0] * es) % 16 == 0 && (st[1] * es) % 16 == 0 &&
                           (st[3] * es) % 16 == 0 && (st[4] * es) % 16 == 0 &&
                           (st[5] * es) % 16 == 0 && (st[7] * es) % 16 == 0 &&
-                          (st[8] * es) % 16 == 0 && (st[9] * es) % 16 == 0;
-  if (!rows_ok || !strides_ok || !al(q) || !al(k_cache) || !al(v_cache)) {
+                          (st[8] * es) % 16 == 0 && (st[9] * es) % 16 == 0 &&
+                          (st[11] * es) % 16 == 0 && (st[12] * es) % 16 == 0;
+  if (!rows_ok || !strides_ok || !al(q) || !al(k_cache) || !al(v_cache) || !al(out)) {
     return fail(MI_ERR_UNSUPPORTED,
-                "mi_paged_decode: q/k_cache/v_cache need a contiguous, 16-byte aligned head_dim "
+                "mi_paged_decode: q/k_cache/v_cache/out need a contiguous, 16-byte aligned head_dim "
                 "(strides q=%lld,%lld,%lld k=%lld,%lld,%lld,%lld)",
                 (long long)st[0], (long long)st[1], (long long)st[2], (long long)st[3],
                 (long long)st[4], (long long)st[5], (long long)st[6]);
@@ -622,7 +713,7 @@ extern "C" int mi_paged_decode(const void* q, const void* k_cache, const void* v
   DecodeArgs a;
   a.B = B; a.H = H; a.H_kv = H_kv; a.G = H / H_kv; a.kvb_log2 = p.kvb_log2;
   a.n_hchunks = p.n_hchunks; a.bs_log2 = bs_log2;
-  a.max_blocks = max_blocks; a.target = kTargetSplits; a.slots = p.slots;
+  a.max_blocks = max_blocks; a.target = p.target; a.slots = p.slots;
   a.qs0 = st[0]; a.qs1 = st[1];
   a.ks0 = st[3]; a.ks1 = st[4]; a.ks2 = st[5];
   a.vs0 = st[7]; a.vs1 = st[8]; a.vs2 = st[9];
