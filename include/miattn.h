@@ -103,16 +103,28 @@ int mi_paged_decode(const void* q, const void* k_cache, const void* v_cache,
  * (total, H, D), all contiguous; bf16 or fp16 (fp32 is MI_ERR_UNSUPPORTED, the same
  * dtype contract as FA2, reference :338-343).
  *   cu_seqlens      device int32 (n_seqs + 1)
- *   tile_schedule   device int32 (n_tiles), built by mi_varlen_schedule
- * The schedule orders query tiles heaviest-first so the causal triangle does not leave a
- * tail of long tiles; it depends only on the segment lengths and H/H_kv, so a caller
- * builds it once per packed group and reuses it for every layer. */
+ *   schedule        device copy of the int32 words mi_varlen_schedule wrote
+ * mi_varlen_schedule (host only) cuts the packed batch into query tiles, splits the
+ * longest causal tiles' key ranges into pieces, and orders the pieces heaviest-first so
+ * the causal triangle does not leave a tail of long tiles; batches whose longest segment
+ * reaches 2048 tokens get 128-row tiles (LDS-ring kernel), others 64-row tiles. Layout:
+ * {n_work, n_merge, n_partials, layout}, then n_work work entries and n_merge merge
+ * entries of two words each; it returns the word count (host_schedule = NULL sizes it).
+ * It depends only on the segment lengths, H and head_dim, so a caller builds it once per
+ * packed group and reuses it for every layer, passing the four header words to
+ * mi_varlen_prefill.
+ * Split pieces write (O, max, sum) partials into the caller's workspace of
+ * mi_varlen_workspace_size() bytes (0 when nothing is split; 16-byte aligned); a second
+ * launch on the same stream merges them. Calls sharing a workspace must be ordered. */
 int mi_varlen_schedule(const int32_t* host_cu_seqlens, int n_seqs, int H, int H_kv,
                        int D, int causal, int32_t* host_schedule, int capacity);
+size_t mi_varlen_workspace_size(const int32_t* host_schedule, int H);
 int mi_varlen_prefill(const void* q, const void* k, const void* v, void* out,
                       const int32_t* cu_seqlens, int n_seqs, int total_tokens,
-                      int max_seqlen, const int32_t* tile_schedule, int n_tiles, int H,
-                      int H_kv, int D, float scale, int causal, int dtype, void* stream);
+                      int max_seqlen, const int32_t* schedule, int n_work, int n_merge,
+                      int n_partials, int layout, int H, int H_kv, int D, float scale,
+                      int causal, int dtype, void* workspace, size_t workspace_bytes,
+                      void* stream);
 
 #ifdef __cplusplus
 }

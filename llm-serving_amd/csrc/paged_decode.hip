@@ -48,7 +48,10 @@ struct DecodeArgs {
   float scale_log2;
 };
 
-constexpr int kThreads = 256;
+#ifndef MIATTN_DECODE_THREADS
+#define MIATTN_DECODE_THREADS 256
+#endif
+constexpr int kThreads = MIATTN_DECODE_THREADS;
 constexpr int kWaves = kThreads / 64;
 
 // Workgroups a launch aims for: 2 per CU of the 256-CU MI355X, all resident at once.

@@ -28,6 +28,7 @@
 //     the query heads of one KV head are dispatched to the same XCD and its K/V tiles are
 //     served from that XCD's L2.
 #include <algorithm>
+#include <climits>
 #include <type_traits>
 #include <vector>
 
@@ -42,6 +43,19 @@ typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
 
 constexpr int kBQ = 64;  // query rows per workgroup (two blocks of 32)
 constexpr int kXcds = 8; // MI355X: 8 XCDs, workgroups dispatched round-robin over them
+// Schedule layout (int32 words): {n_work, n_merge, n_partials, layout = head_dim << 8 |
+// query rows per tile}, then n_work work entries and n_merge merge entries of two words
+// each (see mi_varlen_schedule). 128-row tiles run the ring kernel, 64-row tiles the
+// register-staged kernel.
+constexpr int kSchedHeader = 4;
+// The ring kernel is chosen when the longest segment reaches this many tokens: measured on
+// MI355X (H16/H_kv8/D128 bf16) it is 23% faster on one 4096-token segment, and 7-19%
+// slower on batches of segments up to ~1.7K tokens, where the register-staged kernel's
+// two workgroups per CU overlap each other's start-up and barrier phases.
+constexpr int kRingMinLen = 2048;
+#ifndef MIATTN_PREFILL_SPLIT
+#define MIATTN_PREFILL_SPLIT 1
+#endif
 
 // K/V tiles in flight in registers while a tile is computed: 1 (tile it+1) or 2 (it+1 and
 // it+2; twice the staging registers).
@@ -135,7 +149,7 @@ __global__ __launch_bounds__(Tiles<D>::THREADS, D <= 128 && Tiles<D>::NKS == 2 ?
   const int x = blockIdx.x;
   const int h = (H % kXcds == 0) ? (x % kXcds) * (H / kXcds) + x / kXcds : x;
   const int kvh = h / G;
-  const int entry = sched[blockIdx.y];
+  const int entry = sched[2 * blockIdx.y];  // (seq, tile); this kernel's entries are never split
   const int seq = int(uint32_t(entry) >> 16);
   const int tile = entry & 0xffff;
   const int seq0 = cu[seq];
@@ -439,34 +453,588 @@ __global__ __launch_bounds__(Tiles<D>::THREADS, D <= 128 && Tiles<D>::NKS == 2 ?
   }
 }
 
-int rows_per_tile() { return kBQ; }
+// ---------------------------------------------------------------- ring kernel (D = 64, 128)
+// Eight waves own 128 query rows (4 blocks of 32) x the two 32-key halves of every 64-key
+// tile. K and V tiles stream from global memory straight into LDS (buffer_load_dwordx4 ...
+// lds, no staging registers) through a ring of four stages, so tile it+2 is in flight
+// while tile it is computed and the load latency is spread over two tiles of MFMA work.
+// Each 16-byte chunk of a key row lands at slot chunk ^ sw(row) (see Ring::sw), which
+// keeps the K operand reads and the transposed V reads free of LDS bank conflicts. V stays
+// row-major in LDS; the PV operand V^T is read with ds_read_b64_tr_b16 (lane i of a 16-lane
+// group receives element i%4 of the 8 bytes addressed by lanes 4j + i/4, j = 0..3), and
+// the source rows are chosen so the operand's key order matches the score accumulator.
+#ifndef MIATTN_PREFILL_STAGES
+#define MIATTN_PREFILL_STAGES 4
+#endif
+#ifndef MIATTN_PREFILL_QPW
+#define MIATTN_PREFILL_QPW 1
+#endif
+template <int D>
+struct Ring {
+  static constexpr int QB = 4;                 // query blocks of 32 rows
+  static constexpr int NKS = 2;                // 32-key halves of a tile
+  // Query blocks per wave: every K and V^T operand a wave reads from LDS feeds QPW
+  // blocks' MFMAs. QPW = 2 runs one wave per SIMD with the O accumulators in AGPRs.
+  static constexpr int QPW = MIATTN_PREFILL_QPW;
+  static constexpr int QPAIRS = QB / QPW;      // query-block groups
+  static constexpr int WAVES = QPAIRS * NKS;
+  static constexpr int THREADS = 64 * WAVES;
+  static constexpr int BQ = 32 * QB;           // query rows per workgroup
+  static constexpr int BK = 32 * NKS;          // keys per tile
+  static constexpr int ROWB = D * 2;           // bytes of one key row of one KV head
+  static constexpr int NCH = D / 8;            // 16-byte chunks per row
+  static constexpr int TILEB = BK * ROWB;      // K (or V) bytes per tile
+  static constexpr int STAGEB = 2 * TILEB;     // K then V
+  static constexpr int SEGS = STAGEB / 1024;   // 1 KiB wave-wide loads per stage
+  static constexpr int LPW = SEGS / WAVES;     // of them per wave
+  static constexpr int RPS = 1024 / ROWB;      // key rows per wave-wide load
+  static constexpr int SWB = NCH == 16 ? 4 : NCH == 8 ? 3 : 2;  // log2(NCH)
+  // LDS stages of the K/V ring: tile it+1 resident while tile it is computed, and
+  // NST - 2 more in flight (5 x 32 KiB = the whole 160 KiB at head_dim 128).
+  static constexpr int NST = MIATTN_PREFILL_STAGES;
+  static_assert(NST == 4 || NST == 5, "ring depth");
+  // Slot permutation of row r: its two low bits become the top bits of the slot index.
+  // Bijective on r mod NCH, so 16 consecutive rows read at one chunk hit 16 slots (K
+  // operand), and 4 consecutive rows x 4 chunks read by the transposed V loads hit 16
+  // slots too.
+  static __device__ __forceinline__ int sw(int r) {
+    return ((r & 3) << (SWB - 2)) | ((r >> 2) & ((NCH >> 2) - 1));
+  }
+  static_assert(SEGS % WAVES == 0 && LPW % 2 == 0, "each wave loads whole K and V segments");
+  static_assert(QB * D * 16 * 4 * 2 <= 2 * STAGEB, "key-half merge fits in two stages");
+};
 
-int keys_per_tile(int D) { return D <= 128 ? Tiles<128>::BK : Tiles<256>::BK; }
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4_t lds_short4_t;
+
+// 16 bytes per lane from a buffer straight into LDS: lane l of the wave writes bytes
+// [16l, 16l + 16) after `dst` (the wave-uniform address goes through M0).
+__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t rsrc, lds_void_t* dst, int voffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, dst, 16, voffset, 0, 0, 0);
+}
+
+// s_waitcnt with vmcnt = N and lgkmcnt = 0 (expcnt left alone; gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14));
+}
+// Workgroup barrier without the release/acquire fences of __syncthreads: those would wait
+// for every LDS-bound load in flight, including the tile two steps ahead. The waits that
+// matter are explicit (wait_vm_lgkm0) and the memory clobber keeps LDS accesses on their
+// side of the barrier.
+__device__ __forceinline__ void bare_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+template <typename T, int D>
+__global__ __launch_bounds__(Ring<D>::THREADS, 1) void varlen_prefill_ring_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    T* __restrict__ out, const int32_t* __restrict__ cu, const int32_t* __restrict__ sched,
+    float* __restrict__ partials, int H, int H_kv, int G, float scale_log2, int causal) {
+  using R = Ring<D>;
+  constexpr int KS = D / 16;  // MFMA k-steps over D for S^T
+  constexpr int DB = D / 32;  // 32-row blocks of D for O^T
+  constexpr int NCH = R::NCH, ROWB = R::ROWB, BK = R::BK, LPW = R::LPW, WAVES = R::WAVES;
+  constexpr int QPW = R::QPW;
+  // Separately declared stages: the compiler's wait insertion tells their LDS-bound loads
+  // apart and never holds a read of one stage for the loads into another.
+  constexpr int NST = R::NST;
+  __shared__ __align__(16) uint8_t st0[R::STAGEB];
+  __shared__ __align__(16) uint8_t st1[R::STAGEB];
+  __shared__ __align__(16) uint8_t st2[R::STAGEB];
+  __shared__ __align__(16) uint8_t st3[R::STAGEB];
+  __shared__ __align__(16) uint8_t st4[NST > 4 ? R::STAGEB : 16];
+
+  const int x = blockIdx.x;
+  const int h = (H % kXcds == 0) ? (x % kXcds) * (H / kXcds) + x / kXcds : x;
+  const int kvh = h / G;
+  // work entry: (seq << 16 | tile, split << 28 | (n_split - 1) << 24 | partial slot)
+  const int entry = sched[2 * blockIdx.y];
+  const int piece = sched[2 * blockIdx.y + 1];
+  const int seq = int(uint32_t(entry) >> 16);
+  const int tile = entry & 0xffff;
+  const int split = int(uint32_t(piece) >> 28);
+  const int n_split = ((piece >> 24) & 15) + 1;
+  const int slot = piece & 0xffffff;
+  const int seq0 = cu[seq];
+  const int L = cu[seq + 1] - seq0;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int qp = wave % R::QPAIRS;  // this wave's group of QPW query blocks
+  const int kh = wave / R::QPAIRS;  // key half of every tile
+  const int g = lane >> 5;          // k-group of the MFMA operands
+  const int col = lane & 31;        // query column owned by this lane (in each block)
+  int qrow0[QPW], qi[QPW];
+#pragma unroll
+  for (int j = 0; j < QPW; ++j) {
+    qrow0[j] = tile * R::BQ + (qp * QPW + j) * 32;
+    qi[j] = qrow0[j] + col;
+  }
+
+  const int64_t q_row = int64_t(H) * D;
+  const int64_t kv_row_b = int64_t(H_kv) * ROWB;
+
+  const int q_end = min(L, tile * R::BQ + R::BQ);
+  const int n_all = causal ? (q_end + BK - 1) / BK : (L + BK - 1) / BK;
+  // This piece's key tiles [t_first, t_end): an even share of the tile's n_all.
+  const int t_first = split * n_all / n_split;
+  const int t_end = (split + 1) * n_all / n_split;
+  const int n_it = t_end - t_first;
+
+  uint4 qB[QPW][KS];
+#pragma unroll
+  for (int j = 0; j < QPW; ++j) {
+    const int qc = qi[j] < L ? qi[j] : L - 1;
+    const T* qp_ = q + int64_t(seq0 + qc) * q_row + h * D + g * 8;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qB[j][ks] = load16(qp_ + ks * 16);
+  }
+
+  // Loads of one tile: wave-wide load i of this wave fills 1 KiB segment j = wave + i *
+  // WAVES of the stage (the first half of the segments is K, the second V). Lane t writes
+  // bytes 16t.. of the segment: key row j' * RPS + t / NCH, slot t % NCH, which holds
+  // chunk slot ^ sw(row) of that row.
+  int dma_off[LPW];
+#pragma unroll
+  for (int i = 0; i < LPW; ++i) {
+    const int jj = (wave + i * WAVES) % (R::SEGS / 2);
+    const int r = jj * R::RPS + lane / NCH;
+    // byte offset of this lane's 16 bytes from the tile's first token
+    dma_off[i] = int(r * kv_row_b) + kvh * ROWB + (((lane % NCH) ^ R::sw(r)) << 4);
+  }
+  const char* kseg = reinterpret_cast<const char*>(k) + int64_t(seq0) * kv_row_b;
+  const char* vseg = reinterpret_cast<const char*>(v) + int64_t(seq0) * kv_row_b;
+  // One buffer resource per tile and tensor: base = the tile's first token, size = up to
+  // the segment's end, so rows past the segment read as zero (range-checked in hardware;
+  // they are masked out of the softmax) and the lane offsets above never change.
+  auto tile_rsrc = [&](const char* seg, int t) {
+    // tiles past this piece (issued by the last steps so every step issues alike) get an
+    // empty range: they read as zero without touching memory
+    const int rem = t < t_end ? L - t * BK : 0;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(seg + int64_t(t) * BK * kv_row_b), (short)0,
+                                             rem > 0 ? int(rem * kv_row_b) : 0, 0x00020000);
+  };
+  auto stage_ptr = [&](auto s_c) -> uint8_t* {
+    constexpr int s = decltype(s_c)::value;
+    return s == 0 ? st0 : s == 1 ? st1 : s == 2 ? st2 : s == 3 ? st3 : st4;
+  };
+  auto issue = [&](int t, auto s_c) {
+    uint8_t* dst = stage_ptr(s_c);
+    const auto rk = tile_rsrc(kseg, t);
+    const auto rv = tile_rsrc(vseg, t);
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+      buffer_load_lds16(i < LPW / 2 ? rk : rv,
+                        (lds_void_t*)((__attribute__((address_space(3))) uint8_t*)dst +
+                                      (wave + i * WAVES) % (R::SEGS / 2) * 1024 + (i < LPW / 2 ? 0 : R::TILEB)),
+                        dma_off[i]);
+    }
+  };
+
+  // Loop-invariant LDS byte offsets of this lane's operands within a stage.
+  int k_rd[KS];
+  {
+    const int r = kh * 32 + col;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) k_rd[ks] = r * ROWB + (((ks * 2 + g) ^ R::sw(r)) << 4);
+  }
+  // V^T operand (A of O^T = V^T P^T), k-step t of the wave's 32 keys: the lane's 8 k
+  // positions are keys 16t + 4g + {0..3} and 16t + 8 + 4g + {0..3} (the score
+  // accumulator's rows). Read 1 fetches the first four: source lane l addresses key
+  // 16t + 4(l/32) + (l%16)/4, d = 32db + 16((l/16)%2) + 4(l%4) .. +3; read 2 is 8 keys on.
+  int v_rd[DB][2][2];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int key = kh * 32 + 16 * t + 8 * hh + 4 * g + ((lane & 15) >> 2);
+        const int d0 = db * 32 + ((lane >> 4) & 1) * 16 + 4 * (lane & 3);
+        v_rd[db][t][hh] = R::TILEB + key * ROWB + (((d0 >> 3) ^ R::sw(key)) << 4) + ((d0 >> 2) & 1) * 8;
+      }
+    }
+  }
+
+  floatx16 o[QPW][DB];
+  float m_i[QPW], l_i[QPW];
+#pragma unroll
+  for (int j = 0; j < QPW; ++j) {
+#pragma unroll
+    for (int i = 0; i < DB; ++i) o[j][i] = zero16();
+    m_i[j] = -INFINITY;
+    l_i[j] = 0.0f;
+  }
+
+  // One step's fused block: the V^T operands of tile t, the K fragments and score MFMAs of
+  // tile t+1 (into `nxt`, every K fragment feeding all QPW blocks) and the online softmax
+  // of tile t (from `cur`), which does not depend on them, in one branch-free block that
+  // the scheduler interleaves MFMA / VALU. MASK drops keys past the segment end and above
+  // the diagonal (the boundary tiles); interior tiles skip it.
+  auto fused = [&](int t, auto s_c, auto s_next_c, floatx16 (&cur)[QPW], floatx16 (&nxt)[QPW], auto mask_c,
+                   uint4 (&pB)[QPW][2], uint4 (&vf)[DB][2], float (&alpha)[QPW], bool (&moved)[QPW]) {
+    constexpr bool kMask = decltype(mask_c)::value;
+    const uint8_t* vbase = stage_ptr(s_c);
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2) {
+        const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_short4_t*)((__attribute__((address_space(3))) const uint8_t*)vbase + v_rd[db][t2][0]));
+        const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_short4_t*)((__attribute__((address_space(3))) const uint8_t*)vbase + v_rd[db][t2][1]));
+        const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+        vf[db][t2] = make_uint4(l2.x, l2.y, h2.x, h2.y);
+      }
+    }
+    const uint8_t* kbase = stage_ptr(s_next_c);
+    uint4 kf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) kf[ks] = *reinterpret_cast<const uint4*>(kbase + k_rd[ks]);
+#pragma unroll
+    for (int j = 0; j < QPW; ++j) {
+      floatx16 sacc = zero16();
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) sacc = mfma32<T>(kf[ks], qB[j][ks], sacc);
+      nxt[j] = sacc;
+    }
+
+    const int kb0 = t * BK + kh * 32;
+#pragma unroll
+    for (int j = 0; j < QPW; ++j) {
+      floatx16 sc = cur[j];
+      if constexpr (kMask) {
+        const int lim = (causal ? min(L, qi[j] + 1) : L) - kb0 - g * 4;  // key offsets < lim are valid
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          if ((e >> 2) * 8 + (e & 3) >= lim) sc[e] = -INFINITY;
+        }
+      }
+      float mloc = sc[0];
+#pragma unroll
+      for (int e = 1; e < 16; ++e) mloc = fmaxf(mloc, sc[e]);
+      const float m_tile = fmaxf(mloc, swap32(mloc)) * scale_log2;
+      // Lazy rescaling: the reference max moves only when some query's tile max exceeds
+      // it by more than 2^8 (log2 units); until then p = 2^(s - m) stays <= 256, exact to
+      // the same relative precision in fp32 and in the 16-bit P operand, and O and l keep
+      // one common reference, so the final O / l is unchanged.
+      moved[j] = __any(m_tile > m_i[j] + 8.0f);
+      const float m_new = moved[j] ? fmaxf(m_i[j], m_tile) : m_i[j];
+      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+      alpha[j] = fast_exp2(m_i[j] - m_use);
+      m_i[j] = m_new;
+      float lsum = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float p = fast_exp2(fmaf(sc[e], scale_log2, -m_use));
+        sc[e] = p;
+        lsum += p;
+      }
+      l_i[j] = fmaf(l_i[j], alpha[j], lsum);
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2) {
+        pB[j][t2] = make_uint4(pack2<T>(sc[8 * t2 + 0], sc[8 * t2 + 1]), pack2<T>(sc[8 * t2 + 2], sc[8 * t2 + 3]),
+                               pack2<T>(sc[8 * t2 + 4], sc[8 * t2 + 5]), pack2<T>(sc[8 * t2 + 6], sc[8 * t2 + 7]));
+      }
+    }
+    // LDS reads first (V^T operands, K fragments), some vector work to cover their latency,
+    // then one score MFMA per group of vector instructions.
+    __builtin_amdgcn_sched_group_barrier(0x0100, 4 * DB + KS, 0);
+    __builtin_amdgcn_sched_group_barrier(0x0002, 12, 0);
+#pragma unroll
+    for (int ks = 0; ks < KS * QPW; ++ks) {
+      __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x0002, kMask ? 10 : 6, 0);
+    }
+  };
+
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
+  using S3 = std::integral_constant<int, 3>;
+  using S4 = std::integral_constant<int, 4>;
+  using Yes = std::true_type;
+  using No = std::false_type;
+  // Tiles 0..NST-2 in flight, 0 and 1 waited for; tile 0's scores go first.
+  issue(t_first, S0{});
+  issue(t_first + 1, S1{});
+  issue(t_first + 2, S2{});
+  if constexpr (NST > 4) issue(t_first + 3, S3{});
+  // Q is consumed here so its loads are not outstanding inside the loop (the loop's
+  // explicit waits count only tile loads).
+#pragma unroll
+  for (int j = 0; j < QPW; ++j) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      asm volatile("" ::"v"(qB[j][ks].x), "v"(qB[j][ks].y), "v"(qB[j][ks].z), "v"(qB[j][ks].w));
+    }
+  }
+  wait_vm_lgkm0<(NST - 3) * LPW>();
+  bare_barrier();
+  floatx16 cur[QPW], nxt[QPW];  // scores of tile it, it+1
+  {
+    uint4 kf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) kf[ks] = *reinterpret_cast<const uint4*>(st0 + k_rd[ks]);
+#pragma unroll
+    for (int j = 0; j < QPW; ++j) {
+      cur[j] = zero16();
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) cur[j] = mfma32<T>(kf[ks], qB[j][ks], cur[j]);
+    }
+  }
+
+  // Step it (tile t = t_first + it in stage it % NST with its scores in hand; tile t+1 in
+  // LDS; tiles t+2.. in flight): issue tile t+NST-1 into the stage tile t-1 used; fused
+  // block (scores of tile t+1, softmax of tile t); rescale O if a running max moved; PV of
+  // tile t; wait for this wave's loads of tile t+2; barrier. Tiles past the piece are
+  // loaded too (inside the segment they are real keys, past it they read as zero) and the
+  // scores of the tile after the piece are computed and never used, so no load or MFMA of
+  // a step is conditional on the trip count.
+  auto step = [&](int it, auto s_c) {
+    constexpr int s = decltype(s_c)::value;
+    const int t = t_first + it;
+    issue(t + NST - 1, std::integral_constant<int, (s + NST - 1) % NST>{});
+    // workgroup-uniform: every key of tile t is valid for every query row of the tile
+    const bool interior = (t + 1) * BK <= L && (!causal || (t + 1) * BK - 1 <= tile * R::BQ);
+    uint4 pB[QPW][2];
+    uint4 vf[DB][2];
+    float alpha[QPW];
+    bool moved[QPW];
+    if (interior) {
+      fused(t, s_c, std::integral_constant<int, (s + 1) % NST>{}, cur, nxt, No{}, pB, vf, alpha, moved);
+    } else {
+      fused(t, s_c, std::integral_constant<int, (s + 1) % NST>{}, cur, nxt, Yes{}, pB, vf, alpha, moved);
+    }
+#pragma unroll
+    for (int j = 0; j < QPW; ++j) {
+      if (moved[j]) {
+#pragma unroll
+        for (int i = 0; i < DB; ++i) o[j][i] *= alpha[j];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < QPW; ++j) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2) o[j][db] = mfma32<T>(vf[db][t2], pB[j][t2], o[j][db]);
+      }
+      cur[j] = nxt[j];
+    }
+    if (it + 2 < n_it) wait_vm_lgkm0<(NST - 3) * LPW>(); else wait_vm_lgkm0<(NST - 2) * LPW>();
+    bare_barrier();
+  };
+  int it = 0;
+  for (; it + NST <= n_it; it += NST) {
+    step(it, S0{});
+    step(it + 1, S1{});
+    step(it + 2, S2{});
+    step(it + 3, S3{});
+    if constexpr (NST > 4) step(it + 4, S4{});
+  }
+  if (it < n_it) step(it, S0{});
+  if (it + 1 < n_it) step(it + 1, S1{});
+  if (it + 2 < n_it) step(it + 2, S2{});
+  if constexpr (NST > 4) {
+    if (it + 3 < n_it) step(it + 3, S3{});
+  }
+  // Loads past the end may still be landing in the stages the merge below reuses.
+  wait_vm_lgkm0<0>();
+  bare_barrier();
+
+  // Fold the two key halves of each query block: kh = 1 waves park (O^T, m, l) in the
+  // stages (all tiles are consumed and no load is in flight), kh = 0 waves merge and store.
+#pragma unroll
+  for (int j = 0; j < QPW; ++j) {
+    const int qb = qp * QPW + j;
+    const float l_tot = l_i[j] + swap32(l_i[j]);
+    float* obuf = reinterpret_cast<float*>(qb < 2 ? st0 : st1) + (qb & 1) * (DB * 16 * 64);
+    float* mlbuf = reinterpret_cast<float*>(st2) + qb * 2 * 64;
+    if (kh > 0) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) obuf[(db * 16 + e) * 64 + lane] = o[j][db][e];
+      }
+      mlbuf[lane] = m_i[j];
+      mlbuf[64 + lane] = l_tot;
+    }
+    l_i[j] = l_tot;
+  }
+  __syncthreads();
+  if (kh > 0) return;
+#pragma unroll
+  for (int j = 0; j < QPW; ++j) {
+    const int qb = qp * QPW + j;
+    const float* obuf = reinterpret_cast<const float*>(qb < 2 ? st0 : st1) + (qb & 1) * (DB * 16 * 64);
+    const float* mlbuf = reinterpret_cast<const float*>(st2) + qb * 2 * 64;
+    const float m_p = mlbuf[lane];
+    const float M = fmaxf(m_i[j], m_p);
+    const float M_use = M == -INFINITY ? 0.0f : M;
+    const float w0 = fast_exp2(m_i[j] - M_use);
+    const float w1 = fast_exp2(m_p - M_use);
+    const float l_all = fmaf(mlbuf[64 + lane], w1, l_i[j] * w0);
+    if (n_split > 1) {
+      // this piece's (O relative to M, M, l) for the merge launch; rows past the segment
+      // are written too and never read
+      float* pbase = partials + (int64_t(slot + split) * H + h) * (R::BQ * (D + 2));
+      const int row = qb * 32 + col;
+      float* prow = pbase + row * D;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+#pragma unroll
+        for (int jg = 0; jg < 4; ++jg) {
+          const int d = db * 32 + jg * 8 + g * 4;
+          float4 v4;
+          v4.x = fmaf(obuf[(db * 16 + jg * 4 + 0) * 64 + lane], w1, o[j][db][jg * 4 + 0] * w0);
+          v4.y = fmaf(obuf[(db * 16 + jg * 4 + 1) * 64 + lane], w1, o[j][db][jg * 4 + 1] * w0);
+          v4.z = fmaf(obuf[(db * 16 + jg * 4 + 2) * 64 + lane], w1, o[j][db][jg * 4 + 2] * w0);
+          v4.w = fmaf(obuf[(db * 16 + jg * 4 + 3) * 64 + lane], w1, o[j][db][jg * 4 + 3] * w0);
+          *reinterpret_cast<float4*>(prow + d) = v4;
+        }
+      }
+      if (g == 0) *reinterpret_cast<float2*>(pbase + R::BQ * D + row * 2) = make_float2(M, l_all);
+      continue;
+    }
+    const float inv = 1.0f / fmaxf(l_all, 1e-30f);
+    if (qi[j] < L) {
+      T* op = out + int64_t(seq0 + qi[j]) * q_row + h * D;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        float r[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) r[e] = fmaf(obuf[(db * 16 + e) * 64 + lane], w1, o[j][db][e] * w0) * inv;
+#pragma unroll
+        for (int jg = 0; jg < 4; ++jg) {
+          const int d = db * 32 + jg * 8 + g * 4;
+          const uint2 val = make_uint2(pack2<T>(r[jg * 4 + 0], r[jg * 4 + 1]),
+                                       pack2<T>(r[jg * 4 + 2], r[jg * 4 + 3]));
+          *reinterpret_cast<uint2*>(op + d) = val;
+        }
+      }
+    }
+  }
+}
+
+// Second launch for split query tiles, one workgroup per (head, merge entry, quarter of
+// the tile's rows); each thread owns 32 columns of one row and folds that row over the
+// pieces (log-sum-exp on the stored (M, l)), with every load of all pieces in flight at
+// once, then normalises and writes. Merge entry: (seq << 16 | tile, n_split << 24 |
+// first partial slot).
+constexpr int kMaxSplit = 4;
+template <typename T, int D>
+__global__ __launch_bounds__(256) void varlen_prefill_merge_kernel(
+    const int32_t* __restrict__ cu, const int32_t* __restrict__ merges,
+    const float* __restrict__ partials, T* __restrict__ out, int H) {
+  constexpr int BQ = Ring<D>::BQ;
+  constexpr int CPR = D / 32;            // threads per row
+  constexpr int RPB = 256 / CPR;         // rows per workgroup
+  const int h = blockIdx.x;
+  const int entry = merges[2 * blockIdx.y];
+  const int info = merges[2 * blockIdx.y + 1];
+  const int seq = int(uint32_t(entry) >> 16);
+  const int tile = entry & 0xffff;
+  const int n_split = int(uint32_t(info) >> 24);
+  const int slot = info & 0xffffff;
+  const int seq0 = cu[seq];
+  const int L = cu[seq + 1] - seq0;
+  const int row = blockIdx.z * RPB + threadIdx.x / CPR;
+  const int qi = tile * BQ + row;
+  if (row >= BQ || qi >= L) return;
+  const int d0 = (threadIdx.x % CPR) * 32;
+  const int64_t pstride = int64_t(H) * (BQ * (D + 2));  // between consecutive pieces
+  const float* p0 = partials + (int64_t(slot) * H + h) * (BQ * (D + 2));
+  float2 ml[kMaxSplit];
+  float4 v[kMaxSplit][8];
+#pragma unroll
+  for (int s = 0; s < kMaxSplit; ++s) {
+    const int sc = s < n_split ? s : n_split - 1;  // repeated pieces are weighted out below
+    const float* ps = p0 + sc * pstride;
+    ml[s] = *reinterpret_cast<const float2*>(ps + BQ * D + row * 2);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[s][e] = reinterpret_cast<const float4*>(ps + row * D + d0)[e];
+  }
+  float M = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < kMaxSplit; ++s) M = s < n_split ? fmaxf(M, ml[s].x) : M;
+  const float M_use = M == -INFINITY ? 0.0f : M;
+  float acc[32];
+#pragma unroll
+  for (int e = 0; e < 32; ++e) acc[e] = 0.0f;
+  float l = 0.0f;
+#pragma unroll
+  for (int s = 0; s < kMaxSplit; ++s) {
+    const float w = s < n_split ? fast_exp2(ml[s].x - M_use) : 0.0f;
+    l = fmaf(ml[s].y, w, l);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      acc[4 * e + 0] = fmaf(v[s][e].x, w, acc[4 * e + 0]);
+      acc[4 * e + 1] = fmaf(v[s][e].y, w, acc[4 * e + 1]);
+      acc[4 * e + 2] = fmaf(v[s][e].z, w, acc[4 * e + 2]);
+      acc[4 * e + 3] = fmaf(v[s][e].w, w, acc[4 * e + 3]);
+    }
+  }
+  const float inv = 1.0f / fmaxf(l, 1e-30f);
+  T* op = out + int64_t(seq0 + qi) * H * D + h * D + d0;
+#pragma unroll
+  for (int e = 0; e < 32; e += 8) {
+    *reinterpret_cast<uint4*>(op + e) =
+        make_uint4(pack2<T>(acc[e] * inv, acc[e + 1] * inv), pack2<T>(acc[e + 2] * inv, acc[e + 3] * inv),
+                   pack2<T>(acc[e + 4] * inv, acc[e + 5] * inv), pack2<T>(acc[e + 6] * inv, acc[e + 7] * inv));
+  }
+}
+
+// head_dim 64 and 128 run the ring kernel (128 query rows per workgroup), 256 the
+// register-staged kernel (64 rows); both walk 64-key tiles.
+bool ring_d(int D) { return D == 64 || D == 128; }
+int keys_per_tile() { return Ring<128>::BK; }
+static_assert(Ring<128>::BK == Tiles<256>::BK && Ring<64>::BK == Tiles<128>::BK, "64-key tiles");
 
 template <typename T, int D>
 int launch2(const void* q, const void* k, const void* v, void* out, const int32_t* cu,
-            const int32_t* sched, int n_tiles, int H, int H_kv, float scale_log2, int causal,
-            hipStream_t s) {
-  dim3 grid(H, n_tiles);
-  hipLaunchKernelGGL((varlen_prefill_kernel<T, D>), grid, dim3(Tiles<D>::THREADS), 0, s,
-                     static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
-                     static_cast<T*>(out), cu, sched, H, H_kv, H / H_kv, scale_log2, causal);
+            const int32_t* sched, int n_work, int n_merge, bool ring, float* partials, int H,
+            int H_kv, float scale_log2, int causal, hipStream_t s) {
+  const int32_t* work = sched + kSchedHeader;
+  if (ring) {
+    if constexpr (D == 64 || D == 128) {
+    hipLaunchKernelGGL((varlen_prefill_ring_kernel<T, D>), dim3(H, n_work), dim3(Ring<D>::THREADS), 0, s,
+                       static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
+                       static_cast<T*>(out), cu, work, partials, H, H_kv, H / H_kv, scale_log2, causal);
+    if (n_merge > 0) {
+      constexpr int kRowsPerBlock = 256 / (D / 32);
+      hipLaunchKernelGGL((varlen_prefill_merge_kernel<T, D>),
+                         dim3(H, n_merge, (Ring<D>::BQ + kRowsPerBlock - 1) / kRowsPerBlock), dim3(256), 0, s, cu,
+                         work + 2 * n_work, static_cast<const float*>(partials), static_cast<T*>(out), H);
+    }
+    }
+  } else {
+    hipLaunchKernelGGL((varlen_prefill_kernel<T, D>), dim3(H, n_work), dim3(Tiles<D>::THREADS), 0, s,
+                       static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
+                       static_cast<T*>(out), cu, work, H, H_kv, H / H_kv, scale_log2, causal);
+  }
   return launch_status("mi_varlen_prefill");
 }
 
 template <typename T>
 int launch1(int D, const void* q, const void* k, const void* v, void* out, const int32_t* cu,
-            const int32_t* sched, int n_tiles, int H, int H_kv, float sl2, int causal,
-            hipStream_t s) {
+            const int32_t* sched, int n_work, int n_merge, bool ring, float* partials, int H,
+            int H_kv, float sl2, int causal, hipStream_t s) {
   switch (D) {
-    case 64: return launch2<T, 64>(q, k, v, out, cu, sched, n_tiles, H, H_kv, sl2, causal, s);
-    case 128: return launch2<T, 128>(q, k, v, out, cu, sched, n_tiles, H, H_kv, sl2, causal, s);
-    case 256: return launch2<T, 256>(q, k, v, out, cu, sched, n_tiles, H, H_kv, sl2, causal, s);
+    case 64: return launch2<T, 64>(q, k, v, out, cu, sched, n_work, n_merge, ring, partials, H, H_kv, sl2, causal, s);
+    case 128: return launch2<T, 128>(q, k, v, out, cu, sched, n_work, n_merge, ring, partials, H, H_kv, sl2, causal, s);
+    case 256: return launch2<T, 256>(q, k, v, out, cu, sched, n_work, n_merge, ring, partials, H, H_kv, sl2, causal, s);
   }
   return fail(MI_ERR_UNSUPPORTED,
               "mi_varlen_prefill: head_dim %d is not supported by the HIP prefill kernel "
               "(supported: 64, 128, 256)",
               D);
+}
+
+size_t partial_bytes(int n_partials, int H, int D, int rows) {
+  return size_t(n_partials) * H * rows * (D + 2) * sizeof(float);
 }
 
 }  // namespace
@@ -482,37 +1050,83 @@ extern "C" int mi_varlen_schedule(const int32_t* host_cu_seqlens, int n_seqs, in
     return fail(MI_ERR_INVALID, "mi_varlen_schedule: n_head (%d) must be a multiple of n_kv_head (%d)",
                 H, H_kv);
   }
-  const int RW = rows_per_tile();
-  const int BN = keys_per_tile(D);
-  struct Item { int work, seq, tile; };
-  std::vector<Item> items;
+  int max_len = 0;
+  for (int s = 0; s < n_seqs; ++s) max_len = std::max(max_len, host_cu_seqlens[s + 1] - host_cu_seqlens[s]);
+  const bool ring = ring_d(D) && max_len >= kRingMinLen;
+  const int RW = ring ? Ring<128>::BQ : kBQ;
+  const int BN = keys_per_tile();
+  struct Tile { int work, seq, tile; };
+  std::vector<Tile> tiles;
+  int64_t total = 0;
   for (int s = 0; s < n_seqs; ++s) {
     const int L = host_cu_seqlens[s + 1] - host_cu_seqlens[s];
     if (L <= 0) return fail(MI_ERR_INVALID, "mi_varlen_schedule: segment %d is empty", s);
-    const int tiles = (L + RW - 1) / RW;
-    if (tiles > 65535) return fail(MI_ERR_UNSUPPORTED, "mi_varlen_schedule: segment %d too long", s);
-    for (int t = 0; t < tiles; ++t) {
+    const int n = (L + RW - 1) / RW;
+    if (n > 65535) return fail(MI_ERR_UNSUPPORTED, "mi_varlen_schedule: segment %d too long", s);
+    for (int t = 0; t < n; ++t) {
       const int end = std::min(L, (t + 1) * RW);
       const int work = causal ? (end + BN - 1) / BN : (L + BN - 1) / BN;
-      items.push_back({work, s, t});
+      tiles.push_back({work, s, t});
+      total += work;
     }
   }
-  std::stable_sort(items.begin(), items.end(),
-                   [](const Item& a, const Item& b) { return a.work > b.work; });
-  const int n = int(items.size());
+  // Split-K for launches that cannot fill the MI355X's 256 CUs (fewer query tiles x heads
+  // than CUs, one ring workgroup per CU): the long tiles' key ranges are cut so that no
+  // piece exceeds the even share of the launch over the CUs, none drops below kMinPiece
+  // key tiles, and no tile splits into more than kMaxSplit pieces. A launch that fills
+  // the chip is not split: its pieces would only add per-workgroup start-up and merge
+  // cost (measured slower on the config-3 batch, 46 + 8 us against 42 us unsplit).
+  constexpr int kCUs = 256, kMinPiece = 8;
+  const int64_t share = (total * H + kCUs - 1) / kCUs;
+  const bool underfilled = int64_t(tiles.size()) * H < kCUs;
+  const int cap = underfilled ? int(std::max<int64_t>(share, kMinPiece)) : INT32_MAX;
+  struct Piece { int work, w0, w1; };
+  std::vector<Piece> pieces, merges;
+  int n_partials = 0;
+  for (const Tile& t : tiles) {
+    int ns = ring && MIATTN_PREFILL_SPLIT ? int((int64_t(t.work) + cap - 1) / cap) : 1;
+    ns = std::max(1, std::min(ns, std::min(kMaxSplit, t.work)));
+    const int w0 = (t.seq << 16) | t.tile;
+    const int slot = ns > 1 ? n_partials : 0;
+    for (int sp = 0; sp < ns; ++sp) {
+      const int work = (sp + 1) * t.work / ns - sp * t.work / ns;
+      pieces.push_back({work, w0, int((uint32_t(sp) << 28) | (uint32_t(ns - 1) << 24) | uint32_t(slot))});
+    }
+    if (ns > 1) {
+      merges.push_back({t.work, w0, int((uint32_t(ns) << 24) | uint32_t(slot))});
+      n_partials += ns;
+    }
+  }
+  if (n_partials >= (1 << 24)) return fail(MI_ERR_UNSUPPORTED, "mi_varlen_schedule: too many split tiles");
+  std::stable_sort(pieces.begin(), pieces.end(), [](const Piece& a, const Piece& b) { return a.work > b.work; });
+  const int n_work = int(pieces.size()), n_merge = int(merges.size());
+  const int words = kSchedHeader + 2 * (n_work + n_merge);
   if (host_schedule != nullptr) {
-    if (capacity < n) {
-      return fail(MI_ERR_INVALID, "mi_varlen_schedule: capacity %d < %d tiles", capacity, n);
+    if (capacity < words) {
+      return fail(MI_ERR_INVALID, "mi_varlen_schedule: capacity %d < %d words", capacity, words);
     }
-    for (int i = 0; i < n; ++i) host_schedule[i] = (items[i].seq << 16) | items[i].tile;
+    host_schedule[0] = n_work;
+    host_schedule[1] = n_merge;
+    host_schedule[2] = n_partials;
+    host_schedule[3] = (D << 8) | RW;
+    int32_t* w = host_schedule + kSchedHeader;
+    for (const Piece& pc : pieces) { *w++ = pc.w0; *w++ = pc.w1; }
+    for (const Piece& pc : merges) { *w++ = pc.w0; *w++ = pc.w1; }
   }
-  return n;
+  return words;
+}
+
+extern "C" size_t mi_varlen_workspace_size(const int32_t* host_schedule, int H) {
+  using namespace miattn;
+  if (host_schedule == nullptr || H < 1) return 0;
+  return partial_bytes(host_schedule[2], H, host_schedule[3] >> 8, host_schedule[3] & 0xff);
 }
 
 extern "C" int mi_varlen_prefill(const void* q, const void* k, const void* v, void* out,
                                  const int32_t* cu_seqlens, int n_seqs, int total_tokens,
-                                 int max_seqlen, const int32_t* tile_schedule, int n_tiles, int H,
-                                 int H_kv, int D, float scale, int causal, int dtype,
+                                 int max_seqlen, const int32_t* schedule, int n_work, int n_merge,
+                                 int n_partials, int layout, int H, int H_kv, int D, float scale,
+                                 int causal, int dtype, void* workspace, size_t workspace_bytes,
                                  void* stream) {
   using namespace miattn;
   if (dtype != MI_BF16 && dtype != MI_F16) {
@@ -523,24 +1137,39 @@ extern "C" int mi_varlen_prefill(const void* q, const void* k, const void* v, vo
     return fail(MI_ERR_INVALID, "mi_varlen_prefill: n_head (%d) must be a multiple of n_kv_head (%d)",
                 H, H_kv);
   }
-  if (n_seqs < 1 || total_tokens < 1 || max_seqlen < 1 || n_tiles < 1 || n_tiles > 65535) {
-    return fail(MI_ERR_INVALID, "mi_varlen_prefill: bad sizes n_seqs=%d total=%d max_seqlen=%d tiles=%d",
-                n_seqs, total_tokens, max_seqlen, n_tiles);
+  if (n_seqs < 1 || total_tokens < 1 || max_seqlen < 1 || n_work < 1 || n_work > 65535 ||
+      n_merge < 0 || n_merge > 65535 || n_partials < 0) {
+    return fail(MI_ERR_INVALID,
+                "mi_varlen_prefill: bad sizes n_seqs=%d total=%d max_seqlen=%d work=%d merge=%d",
+                n_seqs, total_tokens, max_seqlen, n_work, n_merge);
   }
   if (q == nullptr || k == nullptr || v == nullptr || out == nullptr || cu_seqlens == nullptr ||
-      tile_schedule == nullptr) {
+      schedule == nullptr) {
     return fail(MI_ERR_INVALID, "mi_varlen_prefill: NULL pointer argument");
   }
+  const int rows = layout & 0xff;
+  const bool ring = rows == Ring<128>::BQ;
+  if ((layout >> 8) != D || (rows != kBQ && !(ring && ring_d(D))) || (n_merge > 0) != (n_partials > 0) ||
+      (n_merge > 0 && !ring)) {
+    return fail(MI_ERR_INVALID, "mi_varlen_prefill: schedule (layout 0x%x) does not match head_dim %d",
+                layout, D);
+  }
+  const size_t need = partial_bytes(n_partials, H, D, rows);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
+    return fail(MI_ERR_WORKSPACE, "mi_varlen_prefill: workspace of %zu bytes needed, got %zu", need,
+                workspace == nullptr ? size_t(0) : workspace_bytes);
+  }
   auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
-  if (!al(q) || !al(k) || !al(v) || !al(out)) {
-    return fail(MI_ERR_UNSUPPORTED, "mi_varlen_prefill: q/k/v/out must be 16-byte aligned");
+  if (!al(q) || !al(k) || !al(v) || !al(out) || (need > 0 && !al(workspace))) {
+    return fail(MI_ERR_UNSUPPORTED, "mi_varlen_prefill: q/k/v/out/workspace must be 16-byte aligned");
   }
   const float sl2 = float(double(scale) * 1.4426950408889634);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  float* partials = static_cast<float*>(workspace);
   if (dtype == MI_BF16) {
-    return launch1<bf16_t>(D, q, k, v, out, cu_seqlens, tile_schedule, n_tiles, H, H_kv, sl2,
-                           causal, s);
+    return launch1<bf16_t>(D, q, k, v, out, cu_seqlens, schedule, n_work, n_merge, ring, partials, H,
+                           H_kv, sl2, causal, s);
   }
-  return launch1<f16_t>(D, q, k, v, out, cu_seqlens, tile_schedule, n_tiles, H, H_kv, sl2,
-                        causal, s);
+  return launch1<f16_t>(D, q, k, v, out, cu_seqlens, schedule, n_work, n_merge, ring, partials, H,
+                        H_kv, sl2, causal, s);
 }

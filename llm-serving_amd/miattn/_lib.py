@@ -68,14 +68,16 @@ SIGNATURES: dict[str, tuple] = {
     "mi_varlen_schedule": (
         _c_int, [_p_int32, _c_int, _c_int, _c_int, _c_int, _c_int, _p_int32, _c_int]
     ),
+    "mi_varlen_workspace_size": (_c_size_t, [_p_int32, _c_int]),
     "mi_varlen_prefill": (
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
-         _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_float, _c_int, _c_int, _c_void_p],
+         _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_int,
+         _c_int, _c_void_p, _c_size_t, _c_void_p],
     ),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 def _load():

@@ -154,7 +154,8 @@ def _resolve_scale(softmax_scale, head_dim: int) -> float:
 
 
 class _ScheduleCache:
-    """Small LRU of ``(device cu_seqlens, device tile schedule, n_tiles)`` per packed group."""
+    """Small LRU of the device ``cu_seqlens``, the device schedule and its header counts
+    (work pieces, merges, partials, workspace bytes) per packed group."""
 
     def __init__(self, capacity: int = 8) -> None:
         self.capacity = capacity
@@ -168,16 +169,18 @@ class _ScheduleCache:
             return hit
         n_seqs = len(bounds) - 1
         host_cu = (ctypes.c_int32 * len(bounds))(*bounds)
-        n_tiles = _lib.lib.mi_varlen_schedule(host_cu, n_seqs, H, H_kv, D, int(causal), None, 0)
-        if n_tiles < 0:
-            _lib.check(n_tiles, "prefill_varlen schedule")
-        host_sched = (ctypes.c_int32 * n_tiles)()
-        rc = _lib.lib.mi_varlen_schedule(host_cu, n_seqs, H, H_kv, D, int(causal), host_sched, n_tiles)
+        words = _lib.lib.mi_varlen_schedule(host_cu, n_seqs, H, H_kv, D, int(causal), None, 0)
+        if words < 0:
+            _lib.check(words, "prefill_varlen schedule")
+        host_sched = (ctypes.c_int32 * words)()
+        rc = _lib.lib.mi_varlen_schedule(host_cu, n_seqs, H, H_kv, D, int(causal), host_sched, words)
         if rc < 0:
             _lib.check(rc, "prefill_varlen schedule")
+        ws_bytes = int(_lib.lib.mi_varlen_workspace_size(host_sched, H))
         cu = torch.tensor(bounds, dtype=torch.int32).to(device)
         sched = torch.frombuffer(bytearray(host_sched), dtype=torch.int32).to(device)
-        entry = (cu, sched, int(n_tiles))
+        entry = (cu, sched, int(host_sched[0]), int(host_sched[1]), int(host_sched[2]), int(host_sched[3]),
+                 ws_bytes)
         self._items[key] = entry
         if len(self._items) > self.capacity:
             self._items.popitem(last=False)
@@ -225,12 +228,16 @@ class HipVarlen:
         v = v.contiguous()
         total, H, D = q.shape
         H_kv = k.size(1)
-        cu, sched, n_tiles = _SCHEDULES.get(bounds, H, H_kv, D, causal, q.device)
+        cu, sched, n_work, n_merge, n_partials, layout, ws_bytes = _SCHEDULES.get(
+            bounds, H, H_kv, D, causal, q.device)
         out = torch.empty_like(q)
+        # split-tile partials, consumed by the merge launch on the same stream
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
         rc = _lib.lib.mi_varlen_prefill(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), cu.data_ptr(),
-            len(bounds) - 1, total, int(max_seqlen), sched.data_ptr(), n_tiles, H, H_kv, D,
-            float(scale), int(bool(causal)), _lib.dtype_code(q.dtype), _lib.current_stream(q.device),
+            len(bounds) - 1, total, int(max_seqlen), sched.data_ptr(), n_work, n_merge, n_partials,
+            layout, H, H_kv, D, float(scale), int(bool(causal)), _lib.dtype_code(q.dtype),
+            ws.data_ptr() if ws is not None else None, ws_bytes, _lib.current_stream(q.device),
         )
         _lib.check(rc, "prefill_varlen")
         return out

@@ -45,25 +45,92 @@ def test_error_channel_reports_the_last_failure():
 
 
 def _schedule(lengths, H=16, H_kv=8, D=128, causal=1):
+    """(header, work pieces, merges) of mi_varlen_schedule: pieces are (seq, tile, split,
+    n_split, slot), merges (seq, tile, n_split, slot)."""
     cu = [0]
     for n in lengths:
         cu.append(cu[-1] + n)
     host_cu = (ctypes.c_int32 * len(cu))(*cu)
-    n = _lib.lib.mi_varlen_schedule(host_cu, len(lengths), H, H_kv, D, causal, None, 0)
-    out = (ctypes.c_int32 * max(n, 1))()
-    assert _lib.lib.mi_varlen_schedule(host_cu, len(lengths), H, H_kv, D, causal, out, n) == n
-    return [(out[i] >> 16, out[i] & 0xFFFF) for i in range(n)]
+    words = _lib.lib.mi_varlen_schedule(host_cu, len(lengths), H, H_kv, D, causal, None, 0)
+    out = (ctypes.c_int32 * words)()
+    assert _lib.lib.mi_varlen_schedule(host_cu, len(lengths), H, H_kv, D, causal, out, words) == words
+    n_work, n_merge, n_partials, layout = out[0], out[1], out[2], out[3]
+    rows = 128 if D in (64, 128) and max(lengths) >= 2048 else 64  # ring kernel from 2048 tokens
+    assert layout == (D << 8) | rows and words == 4 + 2 * (n_work + n_merge)
+    w = [out[i] & 0xFFFFFFFF for i in range(4, words)]
+    pieces = [(w[2 * i] >> 16, w[2 * i] & 0xFFFF, w[2 * i + 1] >> 28, ((w[2 * i + 1] >> 24) & 15) + 1,
+               w[2 * i + 1] & 0xFFFFFF) for i in range(n_work)]
+    merges = [(w[2 * i] >> 16, w[2 * i] & 0xFFFF, w[2 * i + 1] >> 24, w[2 * i + 1] & 0xFFFFFF)
+              for i in range(n_work, n_work + n_merge)]
+    ws = _lib.lib.mi_varlen_workspace_size(out, H)
+    assert ws == n_partials * H * rows * (D + 2) * 4
+    return (n_work, n_merge, n_partials), pieces, merges
 
 
-def test_schedule_covers_every_tile_once_heaviest_first():
-    lengths = [100, 1, 700, 64, 65]
-    rows = 64  # 64 query rows per workgroup (one head, 2 query blocks x 2 key halves)
-    sched = _schedule(lengths)
-    expected = {(s, t) for s, n in enumerate(lengths) for t in range(-(-n // rows))}
-    assert sorted(sched) == sorted(expected)
-    work = [min(lengths[s], (t + 1) * rows) for s, t in sched]
-    kt = [-(-w // 64) for w in work]  # 64-key tiles
-    assert kt == sorted(kt, reverse=True)
+def _tile_work(lengths, s, t, rows, causal=True):
+    end = min(lengths[s], (t + 1) * rows)
+    return -(-(end if causal else lengths[s]) // 64)  # 64-key tiles
+
+
+def _piece_work(lengths, p, rows):
+    s, t, sp, ns, _ = p
+    n = _tile_work(lengths, s, t, rows)
+    return (sp + 1) * n // ns - sp * n // ns
+
+
+@pytest.mark.parametrize("lengths,H,rows", [
+    ([100, 1, 700, 64, 65, 1742, 450], 16, 64),  # longest < 2048: 64-row tiles, never split
+    ([100, 1, 2100, 64, 65], 4, 128),            # ring kernel, underfilled launch: split pieces
+])
+def test_schedule_covers_every_tile_once_heaviest_first(lengths, H, rows):
+    (n_work, n_merge, n_partials), pieces, merges = _schedule(lengths, H=H, H_kv=min(H, 8))
+    # every (tile, split) exactly once; splits of a tile share its n_split and slot
+    seen = {}
+    for s, t, sp, ns, slot in pieces:
+        assert 0 <= sp < ns <= 4 and (s, t, sp) not in seen
+        seen[(s, t, sp)] = (ns, slot)
+    tiles = {(s, t) for s, n in enumerate(lengths) for t in range(-(-n // rows))}
+    assert {(s, t) for s, t, _ in seen} == tiles
+    for s, t in tiles:
+        ns = seen[(s, t, 0)][0]
+        assert all(seen[(s, t, sp)] == seen[(s, t, 0)] for sp in range(ns))
+    # a merge entry for exactly the split tiles, each owning consecutive partial slots
+    split_tiles = {(s, t): seen[(s, t, 0)] for s, t in tiles if seen[(s, t, 0)][0] > 1}
+    assert {(s, t): (ns, slot) for s, t, ns, slot in merges} == split_tiles
+    slots = sorted(slot for _, slot in split_tiles.values())
+    assert slots == [sum(ns for ns, sl in split_tiles.values() if sl < x) for x in slots]
+    assert n_partials == sum(ns for ns, _ in split_tiles.values()) and n_merge == len(merges)
+    # pieces partition their tile's key tiles and come heaviest first
+    work = [_piece_work(lengths, p, rows) for p in pieces]
+    assert all(x > 0 for x in work) and work == sorted(work, reverse=True)
+    assert n_work == len(pieces)
+
+
+def test_schedule_splits_only_launches_that_underfill_the_chip():
+    rows = 128
+    # one 2100-token segment x 8 heads = 136 ring workgroups < 256 CUs: long tiles are cut to
+    # the per-CU share of the work (at least 8 key tiles, at most 4 pieces)
+    lengths, H = [2100], 8
+    _, pieces, merges = _schedule(lengths, H=H, H_kv=4)
+    total = sum(_tile_work(lengths, 0, t, rows) for t in range(-(-lengths[0] // rows)))
+    cap = max(-(-(total * H) // 256), 8)
+    assert merges
+    for p in pieces:
+        n = _tile_work(lengths, p[0], p[1], rows)
+        assert _piece_work(lengths, p, rows) <= max(cap, -(-n // 4))
+    # 4096 tokens at 16 heads fills the chip (32 tiles x 16 heads): no splits; the config-3
+    # batch (longest 1742) takes 64-row tiles, which never split
+    for lengths in ([4096], [1742, 110, 658, 364, 390, 450, 152, 445]):
+        _, pieces, merges = _schedule(lengths, H=16)
+        assert not merges and all(p[3] == 1 for p in pieces)
+
+
+def test_schedule_head_dim_256_uses_64_row_tiles_and_never_splits():
+    lengths = [100, 1700]
+    (_, n_merge, n_partials), pieces, _ = _schedule(lengths, D=256)
+    assert n_merge == 0 and n_partials == 0
+    assert sorted((s, t) for s, t, *_ in pieces) == sorted(
+        {(s, t) for s, n in enumerate(lengths) for t in range(-(-n // 64))})
 
 
 def test_schedule_rejects_empty_segments():

@@ -67,6 +67,26 @@ def test_head_dims_and_dtypes(D, dtype, cuda):
     assert (out.float() - longhand_varlen(q, k, v, cu)).abs().max().item() <= 2e-2
 
 
+@pytest.mark.parametrize("lengths,H,H_kv,D,dtype", [
+    pytest.param([2100], 8, 4, 128, torch.bfloat16, id="ring-split-2100-gqa2"),
+    pytest.param([1, 17, 2048, 300], 16, 8, 128, torch.bfloat16, id="ring-qwen3-4seg"),
+    pytest.param([2049, 33], 8, 1, 64, torch.float16, id="ring-d64-fp16-gqa8"),
+])
+def test_long_segments_take_the_ring_kernel(lengths, H, H_kv, D, dtype, cuda):
+    """Longest segment >= 2048 tokens: 128-row tiles through the LDS-ring kernel, with the
+    long tiles split into pieces and merged when the launch underfills the chip."""
+    q, k, v, cu, ms = _packed(lengths, H, H_kv, D, dtype=dtype, seed=7)
+    out = _run(q, k, v, cu, ms, cuda)
+    assert out.dtype == dtype and torch.isfinite(out).all()
+    assert (out.float() - longhand_varlen(q, k, v, cu)).abs().max().item() <= 2e-2
+
+
+def test_ring_kernel_non_causal(cuda):
+    q, k, v, cu, ms = _packed([2050, 70], 8, 4, 128, seed=8)
+    out = _run(q, k, v, cu, ms, cuda, causal=False)
+    assert (out.float() - longhand_varlen(q, k, v, cu, causal=False)).abs().max().item() <= 2e-2
+
+
 def test_non_causal_and_custom_scale(cuda):
     q, k, v, cu, ms = _packed([17, 64, 200], 8, 1, 128, seed=4)
     out = _run(q, k, v, cu, ms, cuda, causal=False)
