@@ -105,9 +105,13 @@ int mi_paged_decode(const void* q, const void* k_cache, const void* v_cache,
  *   cu_seqlens      device int32 (n_seqs + 1)
  *   schedule        device copy of the int32 words mi_varlen_schedule wrote
  * mi_varlen_schedule (host only) cuts the packed batch into query tiles, splits the
- * longest causal tiles' key ranges into pieces, and orders the pieces heaviest-first so
- * the causal triangle does not leave a tail of long tiles; batches whose longest segment
- * reaches 2048 tokens get 128-row tiles (LDS-ring kernel), others 64-row tiles. Layout:
+ * longest causal tiles' key ranges into pieces when the launch underfills the chip, and
+ * orders the pieces heaviest-first so the causal triangle does not leave a tail of long
+ * tiles. By default head_dim 64/128 batches whose longest segment reaches 2048 tokens run
+ * the LDS-ring kernel (128-row tiles), all others the register-staged kernel (64-row
+ * tiles); mi_varlen_schedule_for names the kernel instead (MI_PREFILL_*; the ring and the
+ * wide kernel -- 64-row tiles, four waves splitting each 128-key step -- take head_dim 64
+ * and 128 only). Layout:
  * {n_work, n_merge, n_partials, layout}, then n_work work entries and n_merge merge
  * entries of two words each; it returns the word count (host_schedule = NULL sizes it).
  * It depends only on the segment lengths, H and head_dim, so a caller builds it once per
@@ -116,8 +120,11 @@ int mi_paged_decode(const void* q, const void* k_cache, const void* v_cache,
  * Split pieces write (O, max, sum) partials into the caller's workspace of
  * mi_varlen_workspace_size() bytes (0 when nothing is split; 16-byte aligned); a second
  * launch on the same stream merges them. Calls sharing a workspace must be ordered. */
+enum { MI_PREFILL_AUTO = -1, MI_PREFILL_STAGED = 0, MI_PREFILL_RING = 1, MI_PREFILL_WIDE = 2 };
 int mi_varlen_schedule(const int32_t* host_cu_seqlens, int n_seqs, int H, int H_kv,
                        int D, int causal, int32_t* host_schedule, int capacity);
+int mi_varlen_schedule_for(const int32_t* host_cu_seqlens, int n_seqs, int H, int H_kv,
+                           int D, int causal, int kernel, int32_t* host_schedule, int capacity);
 size_t mi_varlen_workspace_size(const int32_t* host_schedule, int H);
 int mi_varlen_prefill(const void* q, const void* k, const void* v, void* out,
                       const int32_t* cu_seqlens, int n_seqs, int total_tokens,

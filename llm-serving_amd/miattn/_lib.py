@@ -68,6 +68,9 @@ SIGNATURES: dict[str, tuple] = {
     "mi_varlen_schedule": (
         _c_int, [_p_int32, _c_int, _c_int, _c_int, _c_int, _c_int, _p_int32, _c_int]
     ),
+    "mi_varlen_schedule_for": (
+        _c_int, [_p_int32, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _p_int32, _c_int]
+    ),
     "mi_varlen_workspace_size": (_c_size_t, [_p_int32, _c_int]),
     "mi_varlen_prefill": (
         _c_int,
@@ -77,7 +80,7 @@ SIGNATURES: dict[str, tuple] = {
     ),
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 
 def _load():

@@ -161,19 +161,20 @@ class _ScheduleCache:
         self.capacity = capacity
         self._items: OrderedDict = OrderedDict()
 
-    def get(self, bounds: list[int], H: int, H_kv: int, D: int, causal: bool, device):
-        key = (tuple(bounds), H, H_kv, D, bool(causal), str(device))
+    def get(self, bounds: list[int], H: int, H_kv: int, D: int, causal: bool, device, kernel: int = -1):
+        key = (tuple(bounds), H, H_kv, D, bool(causal), str(device), kernel)
         hit = self._items.get(key)
         if hit is not None:
             self._items.move_to_end(key)
             return hit
         n_seqs = len(bounds) - 1
         host_cu = (ctypes.c_int32 * len(bounds))(*bounds)
-        words = _lib.lib.mi_varlen_schedule(host_cu, n_seqs, H, H_kv, D, int(causal), None, 0)
+        words = _lib.lib.mi_varlen_schedule_for(host_cu, n_seqs, H, H_kv, D, int(causal), kernel, None, 0)
         if words < 0:
             _lib.check(words, "prefill_varlen schedule")
         host_sched = (ctypes.c_int32 * words)()
-        rc = _lib.lib.mi_varlen_schedule(host_cu, n_seqs, H, H_kv, D, int(causal), host_sched, words)
+        rc = _lib.lib.mi_varlen_schedule_for(host_cu, n_seqs, H, H_kv, D, int(causal), kernel, host_sched,
+                                             words)
         if rc < 0:
             _lib.check(rc, "prefill_varlen schedule")
         ws_bytes = int(_lib.lib.mi_varlen_workspace_size(host_sched, H))
@@ -195,8 +196,14 @@ class HipVarlen:
 
     name = "hip-mfma-varlen"
 
-    def __init__(self) -> None:
+    #: kernel names accepted by ``HipVarlen(kernel=...)``; ``None`` lets the library choose
+    KERNELS = {None: -1, "staged": 0, "ring": 1, "wide": 2}
+
+    def __init__(self, kernel: str | None = None) -> None:
         _lib.require_library("the hip-mfma-varlen prefill backend")
+        if kernel not in self.KERNELS:
+            raise ValueError(f"unknown prefill kernel {kernel!r}; choose one of {sorted(k for k in self.KERNELS if k)}")
+        self._kernel = self.KERNELS[kernel]
 
     def prefill_varlen(
         self,
@@ -229,7 +236,7 @@ class HipVarlen:
         total, H, D = q.shape
         H_kv = k.size(1)
         cu, sched, n_work, n_merge, n_partials, layout, ws_bytes = _SCHEDULES.get(
-            bounds, H, H_kv, D, causal, q.device)
+            bounds, H, H_kv, D, causal, q.device, self._kernel)
         out = torch.empty_like(q)
         # split-tile partials, consumed by the merge launch on the same stream
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None

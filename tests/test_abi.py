@@ -44,19 +44,36 @@ def test_error_channel_reports_the_last_failure():
         _lib.check(rc, "probe")
 
 
-def _schedule(lengths, H=16, H_kv=8, D=128, causal=1):
-    """(header, work pieces, merges) of mi_varlen_schedule: pieces are (seq, tile, split,
-    n_split, slot), merges (seq, tile, n_split, slot)."""
+KERNELS = {"staged": 0, "ring": 1, "wide": 2}
+ROWS = {0: 64, 1: 128, 2: 64}   # query rows per tile
+KEYS = {0: 64, 1: 64, 2: 128}   # keys per unit of a tile's work
+
+
+def _kind(kernel, D, lengths=()):
+    if kernel is None:  # ring from a 2048-token segment at head_dim 64/128, staged otherwise
+        return 1 if D in (64, 128) and max(lengths) >= 2048 else 0
+    return KERNELS[kernel]
+
+
+def _schedule(lengths, H=16, H_kv=8, D=128, causal=1, kernel=None):
+    """(header, work pieces, merges) of mi_varlen_schedule_for: pieces are (seq, tile,
+    split, n_split, slot), merges (seq, tile, n_split, slot)."""
     cu = [0]
     for n in lengths:
         cu.append(cu[-1] + n)
     host_cu = (ctypes.c_int32 * len(cu))(*cu)
-    words = _lib.lib.mi_varlen_schedule(host_cu, len(lengths), H, H_kv, D, causal, None, 0)
+    code = -1 if kernel is None else KERNELS[kernel]
+    words = _lib.lib.mi_varlen_schedule_for(host_cu, len(lengths), H, H_kv, D, causal, code, None, 0)
     out = (ctypes.c_int32 * words)()
-    assert _lib.lib.mi_varlen_schedule(host_cu, len(lengths), H, H_kv, D, causal, out, words) == words
+    assert _lib.lib.mi_varlen_schedule_for(host_cu, len(lengths), H, H_kv, D, causal, code, out, words) == words
+    if kernel is None:  # the default entry point makes the same schedule
+        same = (ctypes.c_int32 * words)()
+        assert _lib.lib.mi_varlen_schedule(host_cu, len(lengths), H, H_kv, D, causal, same, words) == words
+        assert list(same) == list(out)
     n_work, n_merge, n_partials, layout = out[0], out[1], out[2], out[3]
-    rows = 128 if D in (64, 128) and max(lengths) >= 2048 else 64  # ring kernel from 2048 tokens
-    assert layout == (D << 8) | rows and words == 4 + 2 * (n_work + n_merge)
+    kind = _kind(kernel, D, lengths)
+    rows = ROWS[kind]
+    assert layout == (kind << 20) | (D << 8) | rows and words == 4 + 2 * (n_work + n_merge)
     w = [out[i] & 0xFFFFFFFF for i in range(4, words)]
     pieces = [(w[2 * i] >> 16, w[2 * i] & 0xFFFF, w[2 * i + 1] >> 28, ((w[2 * i + 1] >> 24) & 15) + 1,
                w[2 * i + 1] & 0xFFFFFF) for i in range(n_work)]
@@ -67,23 +84,27 @@ def _schedule(lengths, H=16, H_kv=8, D=128, causal=1):
     return (n_work, n_merge, n_partials), pieces, merges
 
 
-def _tile_work(lengths, s, t, rows, causal=True):
-    end = min(lengths[s], (t + 1) * rows)
-    return -(-(end if causal else lengths[s]) // 64)  # 64-key tiles
+def _tile_work(lengths, s, t, kind, causal=True):
+    end = min(lengths[s], (t + 1) * ROWS[kind])
+    return -(-(end if causal else lengths[s]) // KEYS[kind])
 
 
-def _piece_work(lengths, p, rows):
+def _piece_work(lengths, p, kind):
     s, t, sp, ns, _ = p
-    n = _tile_work(lengths, s, t, rows)
+    n = _tile_work(lengths, s, t, kind)
     return (sp + 1) * n // ns - sp * n // ns
 
 
-@pytest.mark.parametrize("lengths,H,rows", [
-    ([100, 1, 700, 64, 65, 1742, 450], 16, 64),  # longest < 2048: 64-row tiles, never split
-    ([100, 1, 2100, 64, 65], 4, 128),            # ring kernel, underfilled launch: split pieces
+@pytest.mark.parametrize("lengths,H,kernel", [
+    ([100, 1, 700, 64, 65, 1742, 450], 16, None),     # staged kernel (< 2048 tokens): never split
+    ([100, 1, 700, 64, 65, 1742, 450], 16, "wide"),   # fills the chip: not split
+    ([100, 1, 2100, 64, 65], 4, None),                # ring kernel, underfilled: split pieces
+    ([100, 1, 2100, 64, 65], 2, "wide"),
 ])
-def test_schedule_covers_every_tile_once_heaviest_first(lengths, H, rows):
-    (n_work, n_merge, n_partials), pieces, merges = _schedule(lengths, H=H, H_kv=min(H, 8))
+def test_schedule_covers_every_tile_once_heaviest_first(lengths, H, kernel):
+    (n_work, n_merge, n_partials), pieces, merges = _schedule(lengths, H=H, H_kv=min(H, 8), kernel=kernel)
+    kind = _kind(kernel, 128, lengths)
+    rows = ROWS[kind]
     # every (tile, split) exactly once; splits of a tile share its n_split and slot
     seen = {}
     for s, t, sp, ns, slot in pieces:
@@ -100,28 +121,31 @@ def test_schedule_covers_every_tile_once_heaviest_first(lengths, H, rows):
     slots = sorted(slot for _, slot in split_tiles.values())
     assert slots == [sum(ns for ns, sl in split_tiles.values() if sl < x) for x in slots]
     assert n_partials == sum(ns for ns, _ in split_tiles.values()) and n_merge == len(merges)
+    assert bool(merges) == (kind != 0 and len(tiles) * H < 256)
     # pieces partition their tile's key tiles and come heaviest first
-    work = [_piece_work(lengths, p, rows) for p in pieces]
+    work = [_piece_work(lengths, p, kind) for p in pieces]
     assert all(x > 0 for x in work) and work == sorted(work, reverse=True)
     assert n_work == len(pieces)
 
 
-def test_schedule_splits_only_launches_that_underfill_the_chip():
-    rows = 128
-    # one 2100-token segment x 8 heads = 136 ring workgroups < 256 CUs: long tiles are cut to
-    # the per-CU share of the work (at least 8 key tiles, at most 4 pieces)
-    lengths, H = [2100], 8
-    _, pieces, merges = _schedule(lengths, H=H, H_kv=4)
-    total = sum(_tile_work(lengths, 0, t, rows) for t in range(-(-lengths[0] // rows)))
+@pytest.mark.parametrize("kernel,H", [("ring", 8), ("wide", 4)])
+def test_schedule_splits_only_launches_that_underfill_the_chip(kernel, H):
+    kind = KERNELS[kernel]
+    rows = ROWS[kind]
+    # one 2100-token segment: 17 ring tiles x 8 heads or 33 wide tiles x 4 heads < 256 CUs,
+    # so long tiles are cut to the per-CU share of the work (at least 8 units, at most 4
+    # pieces)
+    lengths = [2100]
+    _, pieces, merges = _schedule(lengths, H=H, H_kv=4, kernel=kernel)
+    total = sum(_tile_work(lengths, 0, t, kind) for t in range(-(-lengths[0] // rows)))
     cap = max(-(-(total * H) // 256), 8)
     assert merges
     for p in pieces:
-        n = _tile_work(lengths, p[0], p[1], rows)
-        assert _piece_work(lengths, p, rows) <= max(cap, -(-n // 4))
-    # 4096 tokens at 16 heads fills the chip (32 tiles x 16 heads): no splits; the config-3
-    # batch (longest 1742) takes 64-row tiles, which never split
+        n = _tile_work(lengths, p[0], p[1], kind)
+        assert _piece_work(lengths, p, kind) <= max(cap, -(-n // 4))
+    # 4096 tokens at 16 heads and the config-3 batch fill the chip: no splits
     for lengths in ([4096], [1742, 110, 658, 364, 390, 450, 152, 445]):
-        _, pieces, merges = _schedule(lengths, H=16)
+        _, pieces, merges = _schedule(lengths, H=16, kernel=kernel)
         assert not merges and all(p[3] == 1 for p in pieces)
 
 
@@ -131,6 +155,13 @@ def test_schedule_head_dim_256_uses_64_row_tiles_and_never_splits():
     assert n_merge == 0 and n_partials == 0
     assert sorted((s, t) for s, t, *_ in pieces) == sorted(
         {(s, t) for s, n in enumerate(lengths) for t in range(-(-n // 64))})
+
+
+def test_schedule_rejects_unknown_kernels_and_head_dims():
+    host_cu = (ctypes.c_int32 * 2)(0, 5)
+    assert _lib.lib.mi_varlen_schedule_for(host_cu, 1, 16, 8, 128, 1, 7, None, 0) == _lib.MI_ERR_INVALID
+    assert _lib.lib.mi_varlen_schedule_for(host_cu, 1, 16, 8, 256, 1, 2, None, 0) == _lib.MI_ERR_UNSUPPORTED
+    assert _lib.lib.mi_varlen_schedule_for(host_cu, 1, 16, 8, 256, 1, 0, None, 0) > 0
 
 
 def test_schedule_rejects_empty_segments():

@@ -3,7 +3,8 @@ varlen tests, reference tests/unit/test_attention_varlen.py:122-544, against thi
 
 Bars: bf16/fp16 max|delta| <= 2e-2 against the fp32 longhand oracle; bitwise packing
 invariance and segment isolation (the kernel's per-tile arithmetic does not depend on the
-other segments of the pack).
+other segments of the pack). Every case runs on the library's default kernel choice and
+on each kernel it can be asked for (``HipVarlen(kernel="ring" | "staged" | "wide")``).
 """
 
 from __future__ import annotations
@@ -41,85 +42,101 @@ def _packed(lengths, H, H_kv, D, *, dtype=torch.bfloat16, seed=0):
     return q, k, v, cu, max(lengths)
 
 
-def _run(q, k, v, cu, max_seqlen, dev, **kw):
-    out = HipVarlen().prefill_varlen(q.to(dev), k.to(dev), v.to(dev), cu_seqlens=cu, max_seqlen=max_seqlen, **kw)
+KERNELS = [pytest.param(None, id="default"), pytest.param("ring", id="ring"), pytest.param("staged", id="staged"),
+           pytest.param("wide", id="wide")]
+
+
+def _run(q, k, v, cu, max_seqlen, dev, kernel=None, **kw):
+    out = HipVarlen(kernel).prefill_varlen(q.to(dev), k.to(dev), v.to(dev), cu_seqlens=cu, max_seqlen=max_seqlen,
+                                           **kw)
     torch.cuda.synchronize()
     return out.cpu()
 
 
+@pytest.mark.parametrize("kernel", KERNELS)
 @pytest.mark.parametrize("H,H_kv", [(8, 4), (8, 1), (16, 8)], ids=["gqa2", "gqa8", "qwen3"])
 @pytest.mark.parametrize("lengths", LENGTH_SETS)
-def test_matches_the_per_segment_oracle(lengths, H, H_kv, cuda):
+def test_matches_the_per_segment_oracle(lengths, H, H_kv, kernel, cuda):
     q, k, v, cu, ms = _packed(lengths, H, H_kv, 128)
-    out = _run(q, k, v, cu, ms, cuda)
+    out = _run(q, k, v, cu, ms, cuda, kernel)
     ref = longhand_varlen(q, k, v, cu)
     assert out.shape == (sum(lengths), H, 128) and out.dtype == torch.bfloat16
     assert torch.isfinite(out).all()
     assert (out.float() - ref).abs().max().item() <= 2e-2
 
 
-@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("D,kernel", [(64, None), (64, "ring"), (64, "staged"), (64, "wide"), (128, None),
+                                      (128, "ring"), (128, "staged"), (128, "wide"), (256, None)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
-def test_head_dims_and_dtypes(D, dtype, cuda):
+def test_head_dims_and_dtypes(D, kernel, dtype, cuda):
     q, k, v, cu, ms = _packed([1, 33, 128, 300], 8, 4, D, dtype=dtype, seed=2)
-    out = _run(q, k, v, cu, ms, cuda)
+    out = _run(q, k, v, cu, ms, cuda, kernel)
     assert out.dtype == dtype
     assert (out.float() - longhand_varlen(q, k, v, cu)).abs().max().item() <= 2e-2
 
 
+@pytest.mark.parametrize("kernel", [pytest.param(None, id="default"), pytest.param("ring", id="ring"),
+                                    pytest.param("wide", id="wide")])
 @pytest.mark.parametrize("lengths,H,H_kv,D,dtype", [
-    pytest.param([2100], 8, 4, 128, torch.bfloat16, id="ring-split-2100-gqa2"),
-    pytest.param([1, 17, 2048, 300], 16, 8, 128, torch.bfloat16, id="ring-qwen3-4seg"),
-    pytest.param([2049, 33], 8, 1, 64, torch.float16, id="ring-d64-fp16-gqa8"),
+    pytest.param([2100], 8, 4, 128, torch.bfloat16, id="split-2100-gqa2"),
+    pytest.param([2100], 2, 1, 128, torch.bfloat16, id="split-2100-h2"),
+    pytest.param([1, 17, 2048, 300], 16, 8, 128, torch.bfloat16, id="qwen3-4seg"),
+    pytest.param([2049, 33], 8, 1, 64, torch.float16, id="d64-fp16-gqa8"),
+    pytest.param([4500], 4, 2, 128, torch.bfloat16, id="split-4500-4way"),
 ])
-def test_long_segments_take_the_ring_kernel(lengths, H, H_kv, D, dtype, cuda):
-    """Longest segment >= 2048 tokens: 128-row tiles through the LDS-ring kernel, with the
-    long tiles split into pieces and merged when the launch underfills the chip."""
+def test_long_segments_and_split_pieces(lengths, H, H_kv, D, dtype, kernel, cuda):
+    """Long segments; when the launch underfills the chip the longest tiles' key ranges
+    are split into pieces whose partials a second launch merges."""
     q, k, v, cu, ms = _packed(lengths, H, H_kv, D, dtype=dtype, seed=7)
-    out = _run(q, k, v, cu, ms, cuda)
+    out = _run(q, k, v, cu, ms, cuda, kernel)
     assert out.dtype == dtype and torch.isfinite(out).all()
     assert (out.float() - longhand_varlen(q, k, v, cu)).abs().max().item() <= 2e-2
 
 
-def test_ring_kernel_non_causal(cuda):
+@pytest.mark.parametrize("kernel", KERNELS)
+def test_long_non_causal(kernel, cuda):
     q, k, v, cu, ms = _packed([2050, 70], 8, 4, 128, seed=8)
-    out = _run(q, k, v, cu, ms, cuda, causal=False)
+    out = _run(q, k, v, cu, ms, cuda, kernel, causal=False)
     assert (out.float() - longhand_varlen(q, k, v, cu, causal=False)).abs().max().item() <= 2e-2
 
 
-def test_non_causal_and_custom_scale(cuda):
+@pytest.mark.parametrize("kernel", KERNELS)
+def test_non_causal_and_custom_scale(kernel, cuda):
     q, k, v, cu, ms = _packed([17, 64, 200], 8, 1, 128, seed=4)
-    out = _run(q, k, v, cu, ms, cuda, causal=False)
+    out = _run(q, k, v, cu, ms, cuda, kernel, causal=False)
     assert (out.float() - longhand_varlen(q, k, v, cu, causal=False)).abs().max().item() <= 2e-2
-    out = _run(q, k, v, cu, ms, cuda, softmax_scale=0.37)
+    out = _run(q, k, v, cu, ms, cuda, kernel, softmax_scale=0.37)
     assert (out.float() - longhand_varlen(q, k, v, cu, scale=0.37)).abs().max().item() <= 2e-2
 
 
-def test_packed_equals_one_at_a_time_bitwise(cuda):
+@pytest.mark.parametrize("kernel", KERNELS)
+def test_packed_equals_one_at_a_time_bitwise(kernel, cuda):
     lengths = [17, 1, 128, 333]
     q, k, v, cu, ms = _packed(lengths, 16, 8, 128, seed=3)
-    packed = _run(q, k, v, cu, ms, cuda)
-    single = torch.cat([_run(q[s:e], k[s:e], v[s:e], [0, e - s], e - s, cuda) for s, e in zip(cu, cu[1:])])
+    packed = _run(q, k, v, cu, ms, cuda, kernel)
+    single = torch.cat([_run(q[s:e], k[s:e], v[s:e], [0, e - s], e - s, cuda, kernel) for s, e in zip(cu, cu[1:])])
     assert torch.equal(packed, single)
 
 
-def test_changing_segment_zero_leaves_the_others_bitwise(cuda):
+@pytest.mark.parametrize("kernel", KERNELS)
+def test_changing_segment_zero_leaves_the_others_bitwise(kernel, cuda):
     lengths = [17, 1, 128]
     q, k, v, cu, ms = _packed(lengths, 8, 4, 128, seed=5)
-    before = _run(q, k, v, cu, ms, cuda)
+    before = _run(q, k, v, cu, ms, cuda, kernel)
     gen = torch.Generator().manual_seed(99)
     q2, k2, v2 = q.clone(), k.clone(), v.clone()
     q2[:17] = torch.randn(17, 8, 128, generator=gen).bfloat16()
     k2[:17] = torch.randn(17, 4, 128, generator=gen).bfloat16()
     v2[:17] = torch.randn(17, 4, 128, generator=gen).bfloat16()
-    after = _run(q2, k2, v2, cu, ms, cuda)
+    after = _run(q2, k2, v2, cu, ms, cuda, kernel)
     assert not torch.equal(after[:17], before[:17])
     assert torch.equal(after[17:], before[17:])
 
 
-def test_config3_full_size(cuda):
+@pytest.mark.parametrize("kernel", KERNELS)
+def test_config3_full_size(kernel, cuda):
     inp = W.prefill_config3()
-    out = _run(inp.q, inp.k, inp.v, inp.cu_seqlens, max(inp.lengths), cuda)
+    out = _run(inp.q, inp.k, inp.v, inp.cu_seqlens, max(inp.lengths), cuda, kernel)
     ref = longhand_varlen(inp.q, inp.k, inp.v, inp.cu_seqlens)
     assert (out.float() - ref).abs().max().item() <= 2e-2
 
@@ -135,5 +152,11 @@ def test_error_surface(cuda):
                                   ([0, 4, 7], 4, "must end at"), ([0, 4, 8], 5, "max_seqlen")):
         with pytest.raises(ValueError, match=match):
             HipVarlen().prefill_varlen(qb.to(cuda), kb.to(cuda), vb.to(cuda), cu_seqlens=bad_cu, max_seqlen=bad_ms)
+    with pytest.raises(ValueError, match="unknown prefill kernel"):
+        HipVarlen("fast")
+    with pytest.raises(ValueError, match="head_dim 64 or 128"):
+        q256 = torch.zeros(8, 8, 256, dtype=torch.bfloat16, device=cuda)
+        k256 = torch.zeros(8, 4, 256, dtype=torch.bfloat16, device=cuda)
+        HipVarlen("wide").prefill_varlen(q256, k256, k256, cu_seqlens=[0, 8], max_seqlen=8)
     assert backend_for("cuda").name == "hip-mfma-varlen"
     assert isinstance(backend_for(torch.device("cuda:0")), HipVarlen)
