@@ -108,19 +108,22 @@ int mi_paged_decode(const void* q, const void* k_cache, const void* v_cache,
  * longest causal tiles' key ranges into pieces when the launch underfills the chip, and
  * orders the pieces heaviest-first so the causal triangle does not leave a tail of long
  * tiles. By default head_dim 64/128 batches whose longest segment reaches 2048 tokens run
- * the LDS-ring kernel (128-row tiles), all others the register-staged kernel (64-row
- * tiles); mi_varlen_schedule_for names the kernel instead (MI_PREFILL_*; the ring and the
- * wide kernel -- 64-row tiles, four waves splitting each 128-key step -- take head_dim 64
- * and 128 only). Layout:
+ * the LDS-ring kernel (128-row tiles), shorter ones the persistent duo kernel (64-row
+ * tiles, two workgroups per CU, each working through its own item list), head_dim 256 the
+ * register-staged kernel (64-row tiles); mi_varlen_schedule_for names the kernel instead
+ * (MI_PREFILL_*; the ring, wide and duo kernels take head_dim 64 and 128 only). Layout of
+ * the staged, ring and wide schedules:
  * {n_work, n_merge, n_partials, layout}, then n_work work entries and n_merge merge
- * entries of two words each; it returns the word count (host_schedule = NULL sizes it).
+ * entries of two words each; the duo schedule is {n_workgroups, n_merge, n_partials,
+ * layout}, n_workgroups {first item word, item count} pairs, the merge entries, then the
+ * items of four words each. It returns the word count (host_schedule = NULL sizes it).
  * It depends only on the segment lengths, H and head_dim, so a caller builds it once per
  * packed group and reuses it for every layer, passing the four header words to
  * mi_varlen_prefill.
  * Split pieces write (O, max, sum) partials into the caller's workspace of
  * mi_varlen_workspace_size() bytes (0 when nothing is split; 16-byte aligned); a second
  * launch on the same stream merges them. Calls sharing a workspace must be ordered. */
-enum { MI_PREFILL_AUTO = -1, MI_PREFILL_STAGED = 0, MI_PREFILL_RING = 1, MI_PREFILL_WIDE = 2 };
+enum { MI_PREFILL_AUTO = -1, MI_PREFILL_STAGED = 0, MI_PREFILL_RING = 1, MI_PREFILL_WIDE = 2, MI_PREFILL_DUO = 3 };
 int mi_varlen_schedule(const int32_t* host_cu_seqlens, int n_seqs, int H, int H_kv,
                        int D, int causal, int32_t* host_schedule, int capacity);
 int mi_varlen_schedule_for(const int32_t* host_cu_seqlens, int n_seqs, int H, int H_kv,

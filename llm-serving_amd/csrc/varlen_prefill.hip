@@ -466,6 +466,9 @@ __global__ __launch_bounds__(Tiles<D>::THREADS, D <= 128 && Tiles<D>::NKS == 2 ?
 #ifndef MIATTN_PREFILL_STAGES
 #define MIATTN_PREFILL_STAGES 4
 #endif
+#ifndef MIATTN_RING_SCHED
+#define MIATTN_RING_SCHED 0
+#endif
 #ifndef MIATTN_PREFILL_QPW
 #define MIATTN_PREFILL_QPW 1
 #endif
@@ -677,22 +680,33 @@ __global__ __launch_bounds__(Ring<D>::THREADS, 1) void varlen_prefill_ring_kerne
                    uint4 (&pB)[QPW][2], uint4 (&vf)[DB][2], float (&alpha)[QPW], bool (&moved)[QPW]) {
     constexpr bool kMask = decltype(mask_c)::value;
     const uint8_t* vbase = stage_ptr(s_c);
-#pragma unroll
-    for (int db = 0; db < DB; ++db) {
-#pragma unroll
-      for (int t2 = 0; t2 < 2; ++t2) {
-        const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_short4_t*)((__attribute__((address_space(3))) const uint8_t*)vbase + v_rd[db][t2][0]));
-        const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_short4_t*)((__attribute__((address_space(3))) const uint8_t*)vbase + v_rd[db][t2][1]));
-        const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
-        vf[db][t2] = make_uint4(l2.x, l2.y, h2.x, h2.y);
-      }
-    }
     const uint8_t* kbase = stage_ptr(s_next_c);
     uint4 kf[KS];
+    auto read_v = [&]() {
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) kf[ks] = *reinterpret_cast<const uint4*>(kbase + k_rd[ks]);
+      for (int db = 0; db < DB; ++db) {
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2) {
+          const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_short4_t*)((__attribute__((address_space(3))) const uint8_t*)vbase + v_rd[db][t2][0]));
+          const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_short4_t*)((__attribute__((address_space(3))) const uint8_t*)vbase + v_rd[db][t2][1]));
+          const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+          vf[db][t2] = make_uint4(l2.x, l2.y, h2.x, h2.y);
+        }
+      }
+    };
+    auto read_k = [&]() {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kf[ks] = *reinterpret_cast<const uint4*>(kbase + k_rd[ks]);
+    };
+#if MIATTN_RING_SCHED == 0
+    read_v();
+    read_k();
+#else
+    read_k();
+    read_v();
+#endif
 #pragma unroll
     for (int j = 0; j < QPW; ++j) {
       floatx16 sacc = zero16();
@@ -739,6 +753,7 @@ __global__ __launch_bounds__(Ring<D>::THREADS, 1) void varlen_prefill_ring_kerne
                                pack2<T>(sc[8 * t2 + 4], sc[8 * t2 + 5]), pack2<T>(sc[8 * t2 + 6], sc[8 * t2 + 7]));
       }
     }
+#if MIATTN_RING_SCHED <= 1
     // LDS reads first (V^T operands, K fragments), some vector work to cover their latency,
     // then one score MFMA per group of vector instructions.
     __builtin_amdgcn_sched_group_barrier(0x0100, 4 * DB + KS, 0);
@@ -748,6 +763,18 @@ __global__ __launch_bounds__(Ring<D>::THREADS, 1) void varlen_prefill_ring_kerne
       __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x0002, kMask ? 10 : 6, 0);
     }
+#elif MIATTN_RING_SCHED == 2
+    // K fragments first, softmax work while they land, V^T reads, then one score MFMA per
+    // group of vector instructions.
+    __builtin_amdgcn_sched_group_barrier(0x0100, KS, 0);
+    __builtin_amdgcn_sched_group_barrier(0x0002, 28, 0);
+    __builtin_amdgcn_sched_group_barrier(0x0100, 4 * DB, 0);
+#pragma unroll
+    for (int ks = 0; ks < KS * QPW; ++ks) {
+      __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x0002, kMask ? 8 : 5, 0);
+    }
+#endif
   };
 
   using S0 = std::integral_constant<int, 0>;
@@ -1301,6 +1328,409 @@ __global__ __launch_bounds__(Wide<D>::THREADS, 1) void varlen_prefill_wide_kerne
   }
 }
 
+// ---------------------------------------------------------------- duo kernel (D = 64, 128)
+// Persistent: the grid is two workgroups per CU, and each works through its own list of
+// items (a 64-row query tile, or a key-range piece of one, of one head), which the host
+// schedule deals out longest-first so every workgroup ends at about the same time, each
+// KV head's items on the XCD whose L2 holds that head's K and V. Four waves own the
+// tile's 64 query rows (two blocks of 32) x the two 32-key halves of every 64-key step;
+// the two workgroups of a CU hide each other's barrier and epilogue phases. K and V go
+// straight from memory into LDS (buffer_load_dwordx4 ... lds, 16-byte chunks swizzled per
+// row, V^T operands read with ds_read_b64_tr_b16) through two rings of two 64-key buffers
+// (64 KiB at head_dim 128, so two workgroups fit the 160 KiB LDS). Step it computes the
+// softmax of tile t (scores in registers), the scores of tile t+1 (K(t+1) resident) and PV
+// of tile t (V(t) resident) while K(t+2) and V(t+1) land in the buffers K(t) and V(t-1)
+// left; one barrier per step. At an item's end the two key halves of each query block fold
+// through the V ring, each wave normalising and storing half of the head dims, while the
+// next item's Q and first two K tiles are already on their way.
+template <int D>
+struct Duo {
+  static constexpr int WAVES = 4;             // 2 query blocks x 2 key halves
+  static constexpr int THREADS = 64 * WAVES;
+  static constexpr int BQ = 64;               // query rows per item
+  static constexpr int BK = 64;               // keys per step
+  static constexpr int ROWB = D * 2;          // bytes of one key row of one KV head
+  static constexpr int NCH = D / 8;           // 16-byte chunks per row
+  static constexpr int BUFB = BK * ROWB;      // bytes of one K (or V) buffer
+  static constexpr int SEGS = BUFB / 1024;    // 1 KiB wave-wide loads per buffer
+  static constexpr int LPW = SEGS / WAVES;    // of them per wave
+  static constexpr int RPS = 1024 / ROWB;     // key rows per wave-wide load
+  static constexpr int SWB = NCH == 16 ? 4 : 3;
+  static constexpr int ITEM_WORDS = 4;        // {seq0, L, tile << 16 | split << 8 | n_split - 1, h << 24 | slot}
+  static_assert(D == 64 || D == 128, "duo kernel head dims");
+  static_assert(SEGS % WAVES == 0 && (WAVES * RPS) % NCH == 0, "whole loads per wave, swizzle invariant");
+  static_assert(2 * (D / 32) * 16 * 64 * 4 <= 2 * BUFB, "fold fits the V ring");
+  static constexpr __host__ __device__ int sw(int r) {
+    return ((r & 3) << (SWB - 2)) | ((r >> 2) & ((NCH >> 2) - 1));
+  }
+};
+
+// s_waitcnt lgkmcnt(0) alone (vmcnt and expcnt left at their maximum).
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14)); }
+
+template <typename T, int D>
+__global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    T* __restrict__ out, const int32_t* __restrict__ sched, float* __restrict__ partials, int H, int H_kv,
+    int G, float scale_log2, int causal) {
+  using W = Duo<D>;
+  constexpr int KS = D / 16;  // MFMA k-steps over D for S^T
+  constexpr int DB = D / 32;  // 32-row blocks of D for O^T
+  constexpr int BK = W::BK, BQ = W::BQ, ROWB = W::ROWB, LPW = W::LPW;
+  __shared__ __align__(16) uint8_t kb0[W::BUFB];
+  __shared__ __align__(16) uint8_t kb1[W::BUFB];
+  __shared__ __align__(16) uint8_t vb0[W::BUFB];
+  __shared__ __align__(16) uint8_t vb1[W::BUFB];
+  __shared__ float mlx[2][2][2][64];  // [key half][query block][m, l][lane]
+
+  // this workgroup's item list: {first word, count}
+  const int first = sched[kSchedHeader + 2 * blockIdx.x];
+  const int count = sched[kSchedHeader + 2 * blockIdx.x + 1];
+  if (count <= 0) return;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int qb = wave & 1;   // query block
+  const int kh = wave >> 1;  // key half of every step
+  const int g = lane >> 5;
+  const int col = lane & 31;
+  const int64_t q_row = int64_t(H) * D;
+  const int64_t kv_row_b = int64_t(H_kv) * ROWB;
+
+  struct Item {
+    int seq0, L, row0, split, n_split, slot, h, t_first, t_end;
+  };
+  // an item's words are loaded (scalar) while the previous item runs, decoded when needed
+  int iw[W::ITEM_WORDS];
+  auto load_words = [&](int i) {
+    const int32_t* w = sched + first + W::ITEM_WORDS * i;
+#pragma unroll
+    for (int j = 0; j < W::ITEM_WORDS; ++j) iw[j] = __builtin_amdgcn_readfirstlane(w[j]);
+  };
+  auto decode = [&]() {
+    Item it;
+    it.seq0 = iw[0];
+    it.L = iw[1];
+    it.row0 = int(uint32_t(iw[2]) >> 16) * BQ;
+    it.split = (iw[2] >> 8) & 0xff;
+    it.n_split = (iw[2] & 0xff) + 1;
+    it.h = int(uint32_t(iw[3]) >> 24);
+    it.slot = iw[3] & 0xffffff;
+    const int q_end = min(it.L, it.row0 + BQ);
+    const int n_all = causal ? (q_end + BK - 1) / BK : (it.L + BK - 1) / BK;
+    it.t_first = it.split * n_all / it.n_split;
+    it.t_end = (it.split + 1) * n_all / it.n_split;
+    return it;
+  };
+
+  // Wave-wide load i of this wave fills 1 KiB segment wave + i * WAVES of a buffer: lane t
+  // writes bytes 16t.. of it, i.e. key row (wave + i * WAVES) * RPS + t / NCH, slot t % NCH,
+  // which holds chunk slot ^ sw(row) of that row; sw(row) is the same for every i, so load
+  // i's lane offset is load 0's plus i * WAVES * RPS rows. One buffer resource per tile:
+  // base = the tile's first token at the item's KV head, range = the tile's rows inside the
+  // segment (rows past it read as zero; a tile past the item reads nothing), so a step
+  // builds two resources and no per-load scalar arithmetic.
+  const int dma_r0 = wave * W::RPS + lane / W::NCH;
+  const int dma_off = int(dma_r0 * kv_row_b) + (((lane % W::NCH) ^ W::sw(dma_r0)) << 4);
+  const int dma_step = int(W::WAVES * W::RPS * kv_row_b);
+  auto issue = [&](const char* seg, const Item& it, int t, uint8_t* dst) {
+    const int rows = t < it.t_end ? min(it.L - t * BK, BK) : 0;
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(seg + int64_t(t) * (BK * kv_row_b)), (short)0,
+                                                      rows * int(kv_row_b), 0x00020000);
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+      buffer_load_lds16(rs, (lds_void_t*)((__attribute__((address_space(3))) uint8_t*)dst + (wave + i * W::WAVES) * 1024),
+                        dma_off + i * dma_step);
+    }
+  };
+  // the item's K and V at its segment's first token and its KV head
+  auto seg_of = [&](const T* base, const Item& it) {
+    return reinterpret_cast<const char*>(base) + int64_t(it.seq0) * kv_row_b + (it.h / G) * ROWB;
+  };
+  uint4 qB[KS];
+  auto load_q = [&](const Item& it) {
+    const int qi = it.row0 + qb * 32 + col;
+    const int qc = qi < it.L ? qi : it.L - 1;
+    const T* qp_ = q + int64_t(it.seq0 + qc) * q_row + it.h * D + g * 8;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qB[ks] = load16(qp_ + ks * 16);
+  };
+
+  // LDS byte offsets of this lane's operands within a buffer (as in the ring kernel): K
+  // fragment of k-step ks, and the two transposed reads of each V^T operand (the second
+  // 16-key k-step sits 16 rows on, which keeps sw(key), so it is a constant offset).
+  int k_rd[KS];
+  {
+    const int r = kh * 32 + col;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) k_rd[ks] = r * ROWB + (((ks * 2 + g) ^ W::sw(r)) << 4);
+  }
+  int v_rd[DB][2];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int key = kh * 32 + 8 * hh + 4 * g + ((lane & 15) >> 2);
+      const int d0 = db * 32 + ((lane >> 4) & 1) * 16 + 4 * (lane & 3);
+      v_rd[db][hh] = key * ROWB + (((d0 >> 3) ^ W::sw(key)) << 4) + ((d0 >> 2) & 1) * 8;
+    }
+  }
+  static_assert(W::sw(16) == W::sw(0) && W::sw(17) == W::sw(1), "16-row shift keeps the swizzle");
+
+  // first item: Q and K(t0), K(t0+1) in flight (later items get them from the epilogue)
+  load_words(0);
+  Item it = decode();
+  const char* kseg = seg_of(k, it);
+  const char* vseg = seg_of(v, it);
+  load_q(it);
+  issue(kseg, it, it.t_first, kb0);
+  issue(kseg, it, it.t_first + 1, kb1);
+
+  for (int idx = 0; idx < count; ++idx) {
+    const int L = it.L;
+    const int qi = it.row0 + qb * 32 + col;
+    const int n_it = it.t_end - it.t_first;
+    if (idx + 1 < count) load_words(idx + 1);  // used by this item's epilogue
+    // Q, K(t0), K(t0+1) (and the previous item's output stores) complete
+    wait_vm_lgkm0<0>();
+    bare_barrier();
+    floatx16 cur;
+    {
+      uint4 kf[KS];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kf[ks] = *reinterpret_cast<const uint4*>(kb0 + k_rd[ks]);
+      cur = zero16();
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) cur = mfma32<T>(kf[ks], qB[ks], cur);
+    }
+    wait_lgkm0();
+    bare_barrier();  // every wave has read K(t0) before step 0 refills its buffer
+
+    floatx16 o[DB];
+#pragma unroll
+    for (int i = 0; i < DB; ++i) o[i] = zero16();
+    float m_i = -INFINITY;
+    float l_i = 0.0f;
+    uint4 pB[2];  // P of the previous tile, whose PV runs in this step
+
+    auto read_vt = [&](const uint8_t* vb, uint4 (&vf)[DB][2]) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2) {
+          const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_short4_t*)((__attribute__((address_space(3))) const uint8_t*)vb + v_rd[db][0] + t2 * 16 * ROWB));
+          const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_short4_t*)((__attribute__((address_space(3))) const uint8_t*)vb + v_rd[db][1] + t2 * 16 * ROWB));
+          const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+          vf[db][t2] = make_uint4(l2.x, l2.y, h2.x, h2.y);
+        }
+      }
+    };
+    // Step sidx (tile t = t_first + sidx): softmax of tile t (its scores in registers), the
+    // scores of tile t+1 (K(t+1) in kb_next) and PV of tile t-1 (V(t-1) in vb_prev, P(t-1)
+    // from the previous step), so every MFMA of the step is independent of the step's
+    // softmax; K(t+2) goes to kb_free (K(t)'s buffer) and V(t) to vb_free (V(t-2)'s). The
+    // first step of an item has no PV (kPV false). Every step runs the masked softmax: an
+    // unmasked copy for interior tiles pushes the kernel past its 256 registers.
+    auto step = [&](int sidx, uint8_t* kb_next, uint8_t* kb_free, const uint8_t* vb_prev, uint8_t* vb_free,
+                    auto pv_c) {
+      constexpr bool kPV = decltype(pv_c)::value;
+      const int t = it.t_first + sidx;
+      issue(kseg, it, t + 2, kb_free);
+      issue(vseg, it, t, vb_free);
+      uint4 kf[KS];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kf[ks] = *reinterpret_cast<const uint4*>(kb_next + k_rd[ks]);
+      uint4 vf[DB][2];
+      if constexpr (kPV) read_vt(vb_prev, vf);
+      // online softmax of tile t (raw score units, scale folded into the exp2 argument),
+      // lazy rescaling as in the ring kernel
+      floatx16 sc = cur;
+      // workgroup-uniform: only a tile that reaches past the segment end or the diagonal
+      // needs the mask
+      if ((t + 1) * BK > L || (causal && (t + 1) * BK - 1 > it.row0)) {
+        const int lim = (causal ? min(L, qi + 1) : L) - (t * BK + kh * 32) - g * 4;  // key offsets < lim are valid
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          if ((e >> 2) * 8 + (e & 3) >= lim) sc[e] = -INFINITY;
+        }
+      }
+      float mloc = sc[0];
+#pragma unroll
+      for (int e = 1; e < 16; ++e) mloc = fmaxf(mloc, sc[e]);
+      const float m_tile = fmaxf(mloc, swap32(mloc)) * scale_log2;
+      const bool moved = __any(m_tile > m_i + 8.0f);
+      const float m_new = moved ? fmaxf(m_i, m_tile) : m_i;
+      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+      const float alpha = fast_exp2(m_i - m_use);
+      m_i = m_new;
+      float lsum = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float p = fast_exp2(fmaf(sc[e], scale_log2, -m_use));
+        sc[e] = p;
+        lsum += p;
+      }
+      l_i = fmaf(l_i, alpha, lsum);
+      floatx16 nxt = zero16();
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) nxt = mfma32<T>(kf[ks], qB[ks], nxt);
+      if constexpr (kPV) {
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+#pragma unroll
+          for (int t2 = 0; t2 < 2; ++t2) o[db] = mfma32<T>(vf[db][t2], pB[t2], o[db]);
+        }
+      }
+      // K fragments first, softmax work while the reads land, V^T reads, then one MFMA per
+      // group of vector instructions
+      __builtin_amdgcn_sched_group_barrier(0x0100, KS, 0);
+      __builtin_amdgcn_sched_group_barrier(0x0002, 20, 0);
+      if constexpr (kPV) __builtin_amdgcn_sched_group_barrier(0x0100, 4 * DB, 0);
+#pragma unroll
+      for (int i = 0; i < (kPV ? 2 : 1) * KS; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x0002, kPV ? 5 : 9, 0);
+      }
+      // O (with PV(t-1) added) moves to tile t's reference max
+      if (moved) {
+#pragma unroll
+        for (int i = 0; i < DB; ++i) o[i] *= alpha;
+      }
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2) {
+        pB[t2] = make_uint4(pack2<T>(sc[8 * t2 + 0], sc[8 * t2 + 1]), pack2<T>(sc[8 * t2 + 2], sc[8 * t2 + 3]),
+                            pack2<T>(sc[8 * t2 + 4], sc[8 * t2 + 5]), pack2<T>(sc[8 * t2 + 6], sc[8 * t2 + 7]));
+      }
+      cur = nxt;
+      wait_vm_lgkm0<0>();
+      bare_barrier();
+    };
+    using NoPV = std::false_type;
+    using PV = std::true_type;
+    step(0, kb1, kb0, vb1, vb0, NoPV{});
+    int sidx = 1;
+    for (; sidx + 2 <= n_it; sidx += 2) {
+      step(sidx, kb0, kb1, vb0, vb1, PV{});
+      step(sidx + 1, kb1, kb0, vb1, vb0, PV{});
+    }
+    if (sidx < n_it) step(sidx, kb0, kb1, vb0, vb1, PV{});
+    // PV of the last tile, whose V landed in buffer (n_it - 1) & 1
+    auto drain = [&](const uint8_t* vb) {
+      uint4 vf[DB][2];
+      read_vt(vb, vf);
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2) o[db] = mfma32<T>(vf[db][t2], pB[t2], o[db]);
+      }
+    };
+    if ((n_it - 1) & 1) {
+      drain(vb1);
+    } else {
+      drain(vb0);
+    }
+
+    // the next item's first two K tiles, in flight during this item's epilogue (its Q goes
+    // into the registers once the fold has released them)
+    const Item cur_it = it;
+    const bool more = idx + 1 < count;
+    if (more) {
+      it = decode();
+      kseg = seg_of(k, it);
+      vseg = seg_of(v, it);
+      issue(kseg, it, it.t_first, kb0);
+      issue(kseg, it, it.t_first + 1, kb1);
+    }
+    wait_lgkm0();
+    bare_barrier();  // every wave has read the last V tile before the fold reuses its buffer
+
+    // Fold the two key halves: wave (qb, kh) finalises head-dim blocks [kh * DB/2, (kh+1) *
+    // DB/2) of its query block and hands its other blocks to its partner through V buffer
+    // qb, as [e][lane] floats (conflict-free). Each query block's code names its buffer at
+    // compile time, so the compiler sees that the fold does not touch the K buffers the
+    // next item's loads are filling and does not wait for them.
+    constexpr int HB = DB / 2;  // head-dim blocks each wave finalises
+    // The epilogue's addresses are rebuilt here from an opaque copy of the lane id: computed
+    // once before the item loop they would stay live through it and be spilled, and a
+    // scratch reload waits (in order) for the next item's loads just issued.
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int e_col = ln & 31, e_g = ln >> 5;
+    const int e_qi = cur_it.row0 + qb * 32 + e_col;
+    const float l_tot = l_i + swap32(l_i);
+    mlx[kh][qb][0][ln] = m_i;
+    mlx[kh][qb][1][ln] = l_tot;
+    static_assert(DB * 16 * 64 * 4 <= W::BUFB, "a query block's fold fits one V buffer");
+    auto fold_out = [&](uint8_t* fbuf_bytes) {
+      float* fbuf = reinterpret_cast<float*>(fbuf_bytes);
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        if (db / HB == kh) continue;  // kept
+#pragma unroll
+        for (int e = 0; e < 16; ++e) fbuf[(db * 16 + e) * 64 + ln] = o[db][e];
+      }
+      wait_lgkm0();
+      bare_barrier();
+      const float m_o = mlx[kh ^ 1][qb][0][ln];
+      const float l_o = mlx[kh ^ 1][qb][1][ln];
+      const float M = fmaxf(m_i, m_o);
+      const float M_use = M == -INFINITY ? 0.0f : M;
+      const float w_me = fast_exp2(m_i - M_use);
+      const float w_o = fast_exp2(m_o - M_use);
+      const float l_all = fmaf(l_o, w_o, l_tot * w_me);
+      const float inv = 1.0f / fmaxf(l_all, 1e-30f);
+#pragma unroll
+      for (int hb = 0; hb < HB; ++hb) {
+        const int db = kh * HB + hb;
+        float r[16];
+        // the kept block, selected with compile-time indices so o stays in registers
+#pragma unroll
+        for (int dd = 0; dd < DB; ++dd) {
+          if (dd == db) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) r[e] = fmaf(fbuf[(dd * 16 + e) * 64 + ln], w_o, o[dd][e] * w_me);
+          }
+        }
+        if (cur_it.n_split > 1) {
+          // this piece's (O relative to M, M, l) for the merge launch; rows past the segment
+          // are written too and never read
+          float* pbase = partials + (int64_t(cur_it.slot + cur_it.split) * H + cur_it.h) * (BQ * (D + 2));
+          const int row = qb * 32 + e_col;
+#pragma unroll
+          for (int jg = 0; jg < 4; ++jg) {
+            const int d = db * 32 + jg * 8 + e_g * 4;
+            *reinterpret_cast<float4*>(pbase + row * D + d) =
+                make_float4(r[jg * 4 + 0], r[jg * 4 + 1], r[jg * 4 + 2], r[jg * 4 + 3]);
+          }
+          if (kh == 0 && hb == 0 && e_g == 0) *reinterpret_cast<float2*>(pbase + BQ * D + row * 2) = make_float2(M, l_all);
+          continue;
+        }
+        if (e_qi < cur_it.L) {
+          T* op = out + int64_t(cur_it.seq0 + e_qi) * q_row + cur_it.h * D;
+#pragma unroll
+          for (int jg = 0; jg < 4; ++jg) {
+            const int d = db * 32 + jg * 8 + e_g * 4;
+            const uint2 val = make_uint2(pack2<T>(r[jg * 4 + 0] * inv, r[jg * 4 + 1] * inv),
+                                         pack2<T>(r[jg * 4 + 2] * inv, r[jg * 4 + 3] * inv));
+            *reinterpret_cast<uint2*>(op + d) = val;
+          }
+        }
+      }
+    };
+    if (qb == 0) {
+      fold_out(vb0);
+    } else {
+      fold_out(vb1);
+    }
+    if (more) load_q(it);
+    wait_lgkm0();
+    bare_barrier();  // the V ring and mlx are read before the next item refills them
+  }
+}
+
 // Second launch for split query tiles, one workgroup per (head, merge entry, quarter of
 // the tile's rows); each thread owns 32 columns of one row and folds that row over the
 // pieces (log-sum-exp on the stored (M, l)), with every load of all pieces in flight at
@@ -1369,16 +1799,21 @@ __global__ __launch_bounds__(256) void varlen_prefill_merge_kernel(
 }
 
 // Schedule layout word: kernel kind << 20 | head_dim << 8 | query rows per tile.
-enum Kind { kStaged = MI_PREFILL_STAGED, kRing = MI_PREFILL_RING, kWide = MI_PREFILL_WIDE };
+enum Kind { kStaged = MI_PREFILL_STAGED, kRing = MI_PREFILL_RING, kWide = MI_PREFILL_WIDE, kDuo = MI_PREFILL_DUO };
 constexpr int layout_word(int kind, int D, int rows) { return (kind << 20) | (D << 8) | rows; }
 constexpr int layout_kind(int layout) { return layout >> 20; }
 constexpr int layout_d(int layout) { return (layout >> 8) & 0xfff; }
 constexpr int layout_rows(int layout) { return layout & 0xff; }
-int kind_rows(int kind) { return kind == kRing ? Ring<128>::BQ : kind == kWide ? Wide<128>::BQ : kBQ; }
+int kind_rows(int kind) {
+  return kind == kRing ? Ring<128>::BQ : kind == kWide ? Wide<128>::BQ : kind == kDuo ? Duo<128>::BQ : kBQ;
+}
 // keys per schedule unit of work (a causal tile's cost is counted in these)
-int kind_keys(int kind) { return kind == kWide ? Wide<128>::BK : Ring<128>::BK; }
+int kind_keys(int kind) { return kind == kWide ? Wide<128>::BK : kind == kDuo ? Duo<128>::BK : Ring<128>::BK; }
+// workgroups one CU holds at once
+int kind_per_cu(int kind) { return kind == kDuo || kind == kStaged ? 2 : 1; }
 static_assert(Ring<128>::BK == Tiles<256>::BK && Ring<64>::BK == Tiles<128>::BK, "64-key tiles");
 static_assert(Wide<64>::BQ == Wide<128>::BQ && Wide<64>::BK == Wide<128>::BK, "wide tile shape");
+static_assert(Duo<64>::BQ == Duo<128>::BQ && Duo<64>::BK == Duo<128>::BK, "duo tile shape");
 
 template <typename T, int D>
 int launch2(const void* q, const void* k, const void* v, void* out, const int32_t* cu,
@@ -1386,7 +1821,7 @@ int launch2(const void* q, const void* k, const void* v, void* out, const int32_
             int H_kv, float scale_log2, int causal, hipStream_t s) {
   const int32_t* work = sched + kSchedHeader;
   if constexpr (D == 64 || D == 128) {
-    if (kind == kRing || kind == kWide) {
+    if (kind == kRing || kind == kWide || kind == kDuo) {
       constexpr int kRowsPerBlock = 256 / (D / 32);
       if (kind == kRing) {
         hipLaunchKernelGGL((varlen_prefill_ring_kernel<T, D>), dim3(H, n_work), dim3(Ring<D>::THREADS), 0, s,
@@ -1395,6 +1830,17 @@ int launch2(const void* q, const void* k, const void* v, void* out, const int32_
         if (n_merge > 0) {
           hipLaunchKernelGGL((varlen_prefill_merge_kernel<T, D, Ring<D>::BQ>),
                              dim3(H, n_merge, (Ring<D>::BQ + kRowsPerBlock - 1) / kRowsPerBlock), dim3(256), 0, s,
+                             cu, work + 2 * n_work, static_cast<const float*>(partials), static_cast<T*>(out), H);
+        }
+      } else if (kind == kDuo) {
+        // n_work persistent workgroups; their item table follows the header, the merge
+        // entries follow the table
+        hipLaunchKernelGGL((varlen_prefill_duo_kernel<T, D>), dim3(n_work), dim3(Duo<D>::THREADS), 0, s,
+                           static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
+                           static_cast<T*>(out), sched, partials, H, H_kv, H / H_kv, scale_log2, causal);
+        if (n_merge > 0) {
+          hipLaunchKernelGGL((varlen_prefill_merge_kernel<T, D, Duo<D>::BQ>),
+                             dim3(H, n_merge, (Duo<D>::BQ + kRowsPerBlock - 1) / kRowsPerBlock), dim3(256), 0, s,
                              cu, work + 2 * n_work, static_cast<const float*>(partials), static_cast<T*>(out), H);
         }
       } else {
@@ -1431,6 +1877,78 @@ int launch1(int D, const void* q, const void* k, const void* v, void* out, const
               D);
 }
 
+// One schedule piece: a query tile's key range (w0 = seq << 16 | tile, w1 = split << 28 |
+// (n_split - 1) << 24 | first partial slot), or a merge entry, with its cost in key tiles.
+struct Piece { int work, w0, w1; };
+
+// Persistent duo kernel schedule: {n_wg, n_merge, n_partials, layout}, then n_wg entries
+// {first item word, item count}, the n_merge merge entries, and the items, Duo::ITEM_WORDS
+// words each. Items are (piece, head) pairs dealt out longest-first to the workgroup with
+// the least work so far (LPT); when the KV heads divide evenly over the XCDs, the items of
+// a KV head go to the workgroups of one XCD (workgroup w runs on XCD w % kXcds), so its K
+// and V stay in that XCD's L2. An item costs its key tiles plus kItemOverhead for its
+// prologue and epilogue.
+int duo_schedule(const int32_t* cu, const std::vector<Piece>& pieces, const std::vector<Piece>& merges,
+                 int n_partials, int H, int H_kv, int D, int32_t* out, int capacity) {
+  constexpr int kCUs = 256, kSlots = 2 * kCUs, kItemOverhead = 2;
+  const int64_t n_items = int64_t(pieces.size()) * H;
+  const int n_wg = int(std::min<int64_t>(kSlots, n_items));
+  const int n_merge = int(merges.size());
+  const int64_t words64 = kSchedHeader + 2 * int64_t(n_wg) + 2 * int64_t(n_merge) + Duo<128>::ITEM_WORDS * n_items;
+  if (words64 > INT32_MAX) return fail(MI_ERR_UNSUPPORTED, "mi_varlen_schedule: schedule too large");
+  const int words = int(words64);
+  if (out == nullptr) return words;
+  if (capacity < words) return fail(MI_ERR_INVALID, "mi_varlen_schedule: capacity %d < %d words", capacity, words);
+  // groups of workgroups that share an L2: one per XCD when the KV heads spread evenly
+  const bool affine = n_wg == kSlots && H_kv % kXcds == 0;
+  const int n_groups = affine ? kXcds : 1;
+  const int G = H / H_kv;
+  std::vector<std::vector<int>> lists(n_wg);
+  std::vector<int64_t> load(n_wg, 0);
+  for (int grp = 0; grp < n_groups; ++grp) {
+    // workgroups of this group, as a min-heap on (load, id)
+    std::vector<std::pair<int64_t, int>> heap;
+    for (int w = grp; w < n_wg; w += n_groups) heap.push_back({0, w});
+    auto cmp = [](const std::pair<int64_t, int>& a, const std::pair<int64_t, int>& b) { return a > b; };
+    std::make_heap(heap.begin(), heap.end(), cmp);
+    for (int p = 0; p < int(pieces.size()); ++p) {  // pieces are sorted longest-first
+      for (int h = 0; h < H; ++h) {
+        if (affine && (h / G) % kXcds != grp) continue;
+        std::pop_heap(heap.begin(), heap.end(), cmp);
+        auto& top = heap.back();
+        lists[top.second].push_back(p * H + h);
+        top.first += pieces[p].work + kItemOverhead;
+        std::push_heap(heap.begin(), heap.end(), cmp);
+      }
+    }
+  }
+  out[0] = n_wg;
+  out[1] = n_merge;
+  out[2] = n_partials;
+  out[3] = layout_word(kDuo, D, Duo<128>::BQ);
+  int32_t* table = out + kSchedHeader;
+  int32_t* mw = table + 2 * n_wg;
+  for (const Piece& pc : merges) { *mw++ = pc.w0; *mw++ = pc.w1; }
+  int item_word = int(mw - out);
+  int32_t* iw = mw;
+  for (int w = 0; w < n_wg; ++w) {
+    table[2 * w] = item_word;
+    table[2 * w + 1] = int(lists[w].size());
+    for (int id : lists[w]) {
+      const Piece& pc = pieces[id / H];
+      const int h = id % H;
+      const int seq = int(uint32_t(pc.w0) >> 16), tile = pc.w0 & 0xffff;
+      const int split = int(uint32_t(pc.w1) >> 28), nsm1 = (pc.w1 >> 24) & 15, slot = pc.w1 & 0xffffff;
+      *iw++ = cu[seq];
+      *iw++ = cu[seq + 1] - cu[seq];
+      *iw++ = int((uint32_t(tile) << 16) | (uint32_t(split) << 8) | uint32_t(nsm1));
+      *iw++ = int((uint32_t(h) << 24) | uint32_t(slot));
+      item_word += Duo<128>::ITEM_WORDS;
+    }
+  }
+  return words;
+}
+
 size_t partial_bytes(int n_partials, int H, int D, int rows) {
   return size_t(n_partials) * H * rows * (D + 2) * sizeof(float);
 }
@@ -1442,7 +1960,7 @@ extern "C" int mi_varlen_schedule_for(const int32_t* host_cu_seqlens, int n_seqs
                                       int D, int causal, int kernel, int32_t* host_schedule,
                                       int capacity) {
   using namespace miattn;
-  if (kernel < MI_PREFILL_AUTO || kernel > MI_PREFILL_WIDE) {
+  if (kernel < MI_PREFILL_AUTO || kernel > MI_PREFILL_DUO) {
     return fail(MI_ERR_INVALID, "mi_varlen_schedule: unknown prefill kernel %d", kernel);
   }
   if (kernel != MI_PREFILL_AUTO && kernel != MI_PREFILL_STAGED && D != 64 && D != 128) {
@@ -1458,12 +1976,15 @@ extern "C" int mi_varlen_schedule_for(const int32_t* host_cu_seqlens, int n_seqs
   }
   int max_len = 0;
   for (int s = 0; s < n_seqs; ++s) max_len = std::max(max_len, host_cu_seqlens[s + 1] - host_cu_seqlens[s]);
+  if (kernel == MI_PREFILL_DUO && H > 255) {
+    return fail(MI_ERR_UNSUPPORTED, "mi_varlen_schedule: the duo kernel takes at most 255 heads, got %d", H);
+  }
   // By default head_dim 64 and 128 run the ring kernel when the longest segment reaches
-  // kRingMinLen tokens and the register-staged kernel otherwise (head_dim 256 always runs
-  // the staged kernel); the caller may name a kernel instead.
+  // kRingMinLen tokens and the persistent duo kernel otherwise (head_dim 256 runs the
+  // register-staged kernel); the caller may name a kernel instead.
   const int kind = kernel == MI_PREFILL_STAGED ? kStaged : kernel == MI_PREFILL_RING ? kRing
-                 : kernel == MI_PREFILL_WIDE ? kWide
-                 : ((D == 64 || D == 128) && max_len >= kRingMinLen) ? kRing : kStaged;
+                 : kernel == MI_PREFILL_WIDE ? kWide : kernel == MI_PREFILL_DUO ? kDuo
+                 : (D == 64 || D == 128) ? (max_len >= kRingMinLen ? kRing : kDuo) : kStaged;
   const bool ring = kind != kStaged;  // one workgroup per CU, split-K capable
   const int RW = kind_rows(kind);
   const int BN = kind_keys(kind);
@@ -1489,10 +2010,10 @@ extern "C" int mi_varlen_schedule_for(const int32_t* host_cu_seqlens, int n_seqs
   // the chip is not split: its pieces would only add per-workgroup start-up and merge
   // cost (measured slower on the config-3 batch, 46 + 8 us against 42 us unsplit).
   constexpr int kCUs = 256, kMinPiece = 8;
-  const int64_t share = (total * H + kCUs - 1) / kCUs;
-  const bool underfilled = int64_t(tiles.size()) * H < kCUs;
+  const int slots = kCUs * kind_per_cu(kind);  // workgroups the chip runs at once
+  const int64_t share = (total * H + slots - 1) / slots;
+  const bool underfilled = int64_t(tiles.size()) * H < slots;
   const int cap = underfilled ? int(std::max<int64_t>(share, kMinPiece)) : INT32_MAX;
-  struct Piece { int work, w0, w1; };
   std::vector<Piece> pieces, merges;
   int n_partials = 0;
   for (const Tile& t : tiles) {
@@ -1511,6 +2032,9 @@ extern "C" int mi_varlen_schedule_for(const int32_t* host_cu_seqlens, int n_seqs
   }
   if (n_partials >= (1 << 24)) return fail(MI_ERR_UNSUPPORTED, "mi_varlen_schedule: too many split tiles");
   std::stable_sort(pieces.begin(), pieces.end(), [](const Piece& a, const Piece& b) { return a.work > b.work; });
+  if (kind == kDuo) {
+    return duo_schedule(host_cu_seqlens, pieces, merges, n_partials, H, H_kv, D, host_schedule, capacity);
+  }
   const int n_work = int(pieces.size()), n_merge = int(merges.size());
   const int words = kSchedHeader + 2 * (n_work + n_merge);
   if (host_schedule != nullptr) {
@@ -1567,8 +2091,8 @@ extern "C" int mi_varlen_prefill(const void* q, const void* k, const void* v, vo
   }
   const int rows = layout_rows(layout);
   const int kind = layout_kind(layout);
-  const bool split_capable = kind == kRing || kind == kWide;
-  if (layout_d(layout) != D || kind < kStaged || kind > kWide || rows != kind_rows(kind) ||
+  const bool split_capable = kind == kRing || kind == kWide || kind == kDuo;
+  if (layout_d(layout) != D || kind < kStaged || kind > kDuo || rows != kind_rows(kind) ||
       (split_capable && D != 64 && D != 128) || (n_merge > 0) != (n_partials > 0) ||
       (n_merge > 0 && !split_capable)) {
     return fail(MI_ERR_INVALID, "mi_varlen_prefill: schedule (layout 0x%x) does not match head_dim %d",

@@ -197,7 +197,7 @@ class HipVarlen:
     name = "hip-mfma-varlen"
 
     #: kernel names accepted by ``HipVarlen(kernel=...)``; ``None`` lets the library choose
-    KERNELS = {None: -1, "staged": 0, "ring": 1, "wide": 2}
+    KERNELS = {None: -1, "staged": 0, "ring": 1, "wide": 2, "duo": 3}
 
     def __init__(self, kernel: str | None = None) -> None:
         _lib.require_library("the hip-mfma-varlen prefill backend")

@@ -44,14 +44,17 @@ def test_error_channel_reports_the_last_failure():
         _lib.check(rc, "probe")
 
 
-KERNELS = {"staged": 0, "ring": 1, "wide": 2}
-ROWS = {0: 64, 1: 128, 2: 64}   # query rows per tile
-KEYS = {0: 64, 1: 64, 2: 128}   # keys per unit of a tile's work
+KERNELS = {"staged": 0, "ring": 1, "wide": 2, "duo": 3}
+ROWS = {0: 64, 1: 128, 2: 64, 3: 64}   # query rows per tile
+KEYS = {0: 64, 1: 64, 2: 128, 3: 64}   # keys per unit of a tile's work
+PER_CU = {0: 2, 1: 1, 2: 1, 3: 2}      # workgroups one CU runs at once
 
 
 def _kind(kernel, D, lengths=()):
-    if kernel is None:  # ring from a 2048-token segment at head_dim 64/128, staged otherwise
-        return 1 if D in (64, 128) and max(lengths) >= 2048 else 0
+    if kernel is None:  # head_dim 64/128: ring from a 2048-token segment, duo below; staged otherwise
+        if D in (64, 128):
+            return 1 if max(lengths) >= 2048 else 3
+        return 0
     return KERNELS[kernel]
 
 
@@ -73,6 +76,8 @@ def _schedule(lengths, H=16, H_kv=8, D=128, causal=1, kernel=None):
     n_work, n_merge, n_partials, layout = out[0], out[1], out[2], out[3]
     kind = _kind(kernel, D, lengths)
     rows = ROWS[kind]
+    if kind == 3:
+        return _duo_schedule(out, words, lengths, cu, H, H_kv, D)
     assert layout == (kind << 20) | (D << 8) | rows and words == 4 + 2 * (n_work + n_merge)
     w = [out[i] & 0xFFFFFFFF for i in range(4, words)]
     pieces = [(w[2 * i] >> 16, w[2 * i] & 0xFFFF, w[2 * i + 1] >> 28, ((w[2 * i + 1] >> 24) & 15) + 1,
@@ -82,6 +87,46 @@ def _schedule(lengths, H=16, H_kv=8, D=128, causal=1, kernel=None):
     ws = _lib.lib.mi_varlen_workspace_size(out, H)
     assert ws == n_partials * H * rows * (D + 2) * 4
     return (n_work, n_merge, n_partials), pieces, merges
+
+
+def _duo_schedule(out, words, lengths, cu, H, H_kv, D):
+    """Parse and check the persistent duo kernel's schedule: {n_wg, n_merge, n_partials,
+    layout}, n_wg {first item word, count} entries, the merges, then 4-word items {seq0, L,
+    tile << 16 | split << 8 | n_split - 1, head << 24 | slot}. Returns the pieces of head 0
+    in the common (seq, tile, split, n_split, slot) form, after checking every head has the
+    same pieces."""
+    n_wg, n_merge, n_partials, layout = out[0], out[1], out[2], out[3]
+    assert layout == (3 << 20) | (D << 8) | 64 and 1 <= n_wg <= 512
+    u = [out[i] & 0xFFFFFFFF for i in range(words)]
+    merges = [(u[4 + 2 * n_wg + 2 * i] >> 16, u[4 + 2 * n_wg + 2 * i] & 0xFFFF, u[5 + 2 * n_wg + 2 * i] >> 24,
+               u[5 + 2 * n_wg + 2 * i] & 0xFFFFFF) for i in range(n_merge)]
+    item_base = 4 + 2 * n_wg + 2 * n_merge
+    seq_of = {c: i for i, c in enumerate(cu[:-1])}
+    per_head = {h: [] for h in range(H)}
+    seen_words = 0
+    for wg in range(n_wg):
+        first, count = out[4 + 2 * wg], out[5 + 2 * wg]
+        assert first == item_base + seen_words and count >= 1
+        costs = []
+        for i in range(count):
+            seq0, L, w2, w3 = (u[first + 4 * i + j] for j in range(4))
+            seq = seq_of[seq0]
+            assert lengths[seq] == L
+            tile, split, ns, h, slot = w2 >> 16, (w2 >> 8) & 0xFF, (w2 & 0xFF) + 1, w3 >> 24, w3 & 0xFFFFFF
+            per_head[h].append((seq, tile, split, ns, slot))
+            if n_wg == 512 and H_kv % 8 == 0:  # a KV head's items stay on one XCD
+                assert (h // (H // H_kv)) % 8 == wg % 8
+            costs.append(_piece_work(lengths, (seq, tile, split, ns, slot), 3))
+        assert costs == sorted(costs, reverse=True)  # longest first within a workgroup
+        seen_words += 4 * count
+    assert item_base + seen_words == words
+    pieces = sorted(per_head[0])
+    assert all(sorted(per_head[h]) == pieces for h in range(H))
+    ws = _lib.lib.mi_varlen_workspace_size(out, H)
+    assert ws == n_partials * H * 64 * (D + 2) * 4
+    # in the common form the caller's checks expect: longest first
+    pieces.sort(key=lambda p: -_piece_work(lengths, p, 3))
+    return (len(pieces), n_merge, n_partials), pieces, merges
 
 
 def _tile_work(lengths, s, t, kind, causal=True):
@@ -96,10 +141,12 @@ def _piece_work(lengths, p, kind):
 
 
 @pytest.mark.parametrize("lengths,H,kernel", [
-    ([100, 1, 700, 64, 65, 1742, 450], 16, None),     # staged kernel (< 2048 tokens): never split
+    ([100, 1, 700, 64, 65, 1742, 450], 16, None),     # duo kernel (< 2048 tokens), fills the chip
+    ([100, 1, 700, 64, 65, 1742, 450], 16, "staged"),
     ([100, 1, 700, 64, 65, 1742, 450], 16, "wide"),   # fills the chip: not split
     ([100, 1, 2100, 64, 65], 4, None),                # ring kernel, underfilled: split pieces
     ([100, 1, 2100, 64, 65], 2, "wide"),
+    ([100, 1, 2100, 64, 65], 4, "duo"),
 ])
 def test_schedule_covers_every_tile_once_heaviest_first(lengths, H, kernel):
     (n_work, n_merge, n_partials), pieces, merges = _schedule(lengths, H=H, H_kv=min(H, 8), kernel=kernel)
@@ -121,14 +168,14 @@ def test_schedule_covers_every_tile_once_heaviest_first(lengths, H, kernel):
     slots = sorted(slot for _, slot in split_tiles.values())
     assert slots == [sum(ns for ns, sl in split_tiles.values() if sl < x) for x in slots]
     assert n_partials == sum(ns for ns, _ in split_tiles.values()) and n_merge == len(merges)
-    assert bool(merges) == (kind != 0 and len(tiles) * H < 256)
+    assert bool(merges) == (kind != 0 and len(tiles) * H < 256 * PER_CU[kind])
     # pieces partition their tile's key tiles and come heaviest first
     work = [_piece_work(lengths, p, kind) for p in pieces]
     assert all(x > 0 for x in work) and work == sorted(work, reverse=True)
     assert n_work == len(pieces)
 
 
-@pytest.mark.parametrize("kernel,H", [("ring", 8), ("wide", 4)])
+@pytest.mark.parametrize("kernel,H", [("ring", 8), ("wide", 4), ("duo", 8)])
 def test_schedule_splits_only_launches_that_underfill_the_chip(kernel, H):
     kind = KERNELS[kernel]
     rows = ROWS[kind]
@@ -138,7 +185,7 @@ def test_schedule_splits_only_launches_that_underfill_the_chip(kernel, H):
     lengths = [2100]
     _, pieces, merges = _schedule(lengths, H=H, H_kv=4, kernel=kernel)
     total = sum(_tile_work(lengths, 0, t, kind) for t in range(-(-lengths[0] // rows)))
-    cap = max(-(-(total * H) // 256), 8)
+    cap = max(-(-(total * H) // (256 * PER_CU[kind])), 8)
     assert merges
     for p in pieces:
         n = _tile_work(lengths, p[0], p[1], kind)
@@ -160,6 +207,7 @@ def test_schedule_head_dim_256_uses_64_row_tiles_and_never_splits():
 def test_schedule_rejects_unknown_kernels_and_head_dims():
     host_cu = (ctypes.c_int32 * 2)(0, 5)
     assert _lib.lib.mi_varlen_schedule_for(host_cu, 1, 16, 8, 128, 1, 7, None, 0) == _lib.MI_ERR_INVALID
+    assert _lib.lib.mi_varlen_schedule_for(host_cu, 1, 16, 8, 128, 1, -2, None, 0) == _lib.MI_ERR_INVALID
     assert _lib.lib.mi_varlen_schedule_for(host_cu, 1, 16, 8, 256, 1, 2, None, 0) == _lib.MI_ERR_UNSUPPORTED
     assert _lib.lib.mi_varlen_schedule_for(host_cu, 1, 16, 8, 256, 1, 0, None, 0) > 0
 

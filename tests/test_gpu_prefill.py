@@ -4,7 +4,7 @@ varlen tests, reference tests/unit/test_attention_varlen.py:122-544, against thi
 Bars: bf16/fp16 max|delta| <= 2e-2 against the fp32 longhand oracle; bitwise packing
 invariance and segment isolation (the kernel's per-tile arithmetic does not depend on the
 other segments of the pack). Every case runs on the library's default kernel choice and
-on each kernel it can be asked for (``HipVarlen(kernel="ring" | "staged" | "wide")``).
+on each kernel it can be asked for (``HipVarlen(kernel="ring" | "staged" | "wide" | "duo")``).
 """
 
 from __future__ import annotations
@@ -43,7 +43,7 @@ def _packed(lengths, H, H_kv, D, *, dtype=torch.bfloat16, seed=0):
 
 
 KERNELS = [pytest.param(None, id="default"), pytest.param("ring", id="ring"), pytest.param("staged", id="staged"),
-           pytest.param("wide", id="wide")]
+           pytest.param("wide", id="wide"), pytest.param("duo", id="duo")]
 
 
 def _run(q, k, v, cu, max_seqlen, dev, kernel=None, **kw):
@@ -65,8 +65,9 @@ def test_matches_the_per_segment_oracle(lengths, H, H_kv, kernel, cuda):
     assert (out.float() - ref).abs().max().item() <= 2e-2
 
 
-@pytest.mark.parametrize("D,kernel", [(64, None), (64, "ring"), (64, "staged"), (64, "wide"), (128, None),
-                                      (128, "ring"), (128, "staged"), (128, "wide"), (256, None)])
+@pytest.mark.parametrize("D,kernel", [(64, None), (64, "ring"), (64, "staged"), (64, "wide"), (64, "duo"),
+                                      (128, None), (128, "ring"), (128, "staged"), (128, "wide"), (128, "duo"),
+                                      (256, None)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 def test_head_dims_and_dtypes(D, kernel, dtype, cuda):
     q, k, v, cu, ms = _packed([1, 33, 128, 300], 8, 4, D, dtype=dtype, seed=2)
@@ -76,7 +77,7 @@ def test_head_dims_and_dtypes(D, kernel, dtype, cuda):
 
 
 @pytest.mark.parametrize("kernel", [pytest.param(None, id="default"), pytest.param("ring", id="ring"),
-                                    pytest.param("wide", id="wide")])
+                                    pytest.param("wide", id="wide"), pytest.param("duo", id="duo")])
 @pytest.mark.parametrize("lengths,H,H_kv,D,dtype", [
     pytest.param([2100], 8, 4, 128, torch.bfloat16, id="split-2100-gqa2"),
     pytest.param([2100], 2, 1, 128, torch.bfloat16, id="split-2100-h2"),
