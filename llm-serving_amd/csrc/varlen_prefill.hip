@@ -1664,18 +1664,21 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
     mlx[kh][qb][0][ln] = m_i;
     mlx[kh][qb][1][ln] = l_tot;
     static_assert(DB * 16 * 64 * 4 <= W::BUFB, "a query block's fold fits one V buffer");
-    auto fold_out = [&](uint8_t* fbuf_bytes) {
+    // KH (this wave's key half) is a template argument so that every o[] index below is a
+    // compile-time constant (a run-time block choice compiles to a chain of branches).
+    auto fold_out = [&](uint8_t* fbuf_bytes, auto kh_c) {
+      constexpr int KH = decltype(kh_c)::value;
       float* fbuf = reinterpret_cast<float*>(fbuf_bytes);
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        if (db / HB == kh) continue;  // kept
+        if (db / HB == KH) continue;  // kept
 #pragma unroll
         for (int e = 0; e < 16; ++e) fbuf[(db * 16 + e) * 64 + ln] = o[db][e];
       }
       wait_lgkm0();
       bare_barrier();
-      const float m_o = mlx[kh ^ 1][qb][0][ln];
-      const float l_o = mlx[kh ^ 1][qb][1][ln];
+      const float m_o = mlx[KH ^ 1][qb][0][ln];
+      const float l_o = mlx[KH ^ 1][qb][1][ln];
       const float M = fmaxf(m_i, m_o);
       const float M_use = M == -INFINITY ? 0.0f : M;
       const float w_me = fast_exp2(m_i - M_use);
@@ -1684,16 +1687,10 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
       const float inv = 1.0f / fmaxf(l_all, 1e-30f);
 #pragma unroll
       for (int hb = 0; hb < HB; ++hb) {
-        const int db = kh * HB + hb;
+        const int db = KH * HB + hb;
         float r[16];
-        // the kept block, selected with compile-time indices so o stays in registers
 #pragma unroll
-        for (int dd = 0; dd < DB; ++dd) {
-          if (dd == db) {
-#pragma unroll
-            for (int e = 0; e < 16; ++e) r[e] = fmaf(fbuf[(dd * 16 + e) * 64 + ln], w_o, o[dd][e] * w_me);
-          }
-        }
+        for (int e = 0; e < 16; ++e) r[e] = fmaf(fbuf[(db * 16 + e) * 64 + ln], w_o, o[db][e] * w_me);
         if (cur_it.n_split > 1) {
           // this piece's (O relative to M, M, l) for the merge launch; rows past the segment
           // are written too and never read
@@ -1705,7 +1702,7 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
             *reinterpret_cast<float4*>(pbase + row * D + d) =
                 make_float4(r[jg * 4 + 0], r[jg * 4 + 1], r[jg * 4 + 2], r[jg * 4 + 3]);
           }
-          if (kh == 0 && hb == 0 && e_g == 0) *reinterpret_cast<float2*>(pbase + BQ * D + row * 2) = make_float2(M, l_all);
+          if (KH == 0 && hb == 0 && e_g == 0) *reinterpret_cast<float2*>(pbase + BQ * D + row * 2) = make_float2(M, l_all);
           continue;
         }
         if (e_qi < cur_it.L) {
@@ -1720,10 +1717,12 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
         }
       }
     };
+    using K0 = std::integral_constant<int, 0>;
+    using K1 = std::integral_constant<int, 1>;
     if (qb == 0) {
-      fold_out(vb0);
+      if (kh == 0) fold_out(vb0, K0{}); else fold_out(vb0, K1{});
     } else {
-      fold_out(vb1);
+      if (kh == 0) fold_out(vb1, K0{}); else fold_out(vb1, K1{});
     }
     if (more) load_q(it);
     wait_lgkm0();
@@ -1890,7 +1889,7 @@ struct Piece { int work, w0, w1; };
 // prologue and epilogue.
 int duo_schedule(const int32_t* cu, const std::vector<Piece>& pieces, const std::vector<Piece>& merges,
                  int n_partials, int H, int H_kv, int D, int32_t* out, int capacity) {
-  constexpr int kCUs = 256, kSlots = 2 * kCUs, kItemOverhead = 2;
+  constexpr int kCUs = 256, kSlots = 2 * kCUs, kItemOverhead = 3;
   const int64_t n_items = int64_t(pieces.size()) * H;
   const int n_wg = int(std::min<int64_t>(kSlots, n_items));
   const int n_merge = int(merges.size());

@@ -161,3 +161,38 @@ def test_error_surface(cuda):
         HipVarlen("wide").prefill_varlen(q256, k256, k256, cu_seqlens=[0, 8], max_seqlen=8)
     assert backend_for("cuda").name == "hip-mfma-varlen"
     assert isinstance(backend_for(torch.device("cuda:0")), HipVarlen)
+
+
+@pytest.mark.parametrize("lengths,H,H_kv", [
+    pytest.param([1742, 110, 658, 364, 390, 450, 152, 445], 16, 8, id="config3-per-xcd-lists"),
+    pytest.param([300, 47, 1000], 8, 2, id="one-list"),
+])
+def test_duo_is_stable_across_calls_and_graph_replays(lengths, H, H_kv, cuda):
+    """The persistent duo kernel's workgroups each work through a list of items with the
+    next item's loads in flight during the current one's epilogue: every call must
+    compute every item (outputs match the oracle) and give the same bits call after call,
+    eager and replayed from a HIP graph."""
+    q, k, v, cu, ms = _packed(lengths, H, H_kv, 128, seed=11)
+    qd, kd, vd = q.to(cuda), k.to(cuda), v.to(cuda)
+    be = HipVarlen("duo")
+    first = be.prefill_varlen(qd, kd, vd, cu_seqlens=cu, max_seqlen=ms)
+    torch.cuda.synchronize()
+    assert (first.float().cpu() - longhand_varlen(q, k, v, cu)).abs().max().item() <= 2e-2
+    for _ in range(3):
+        again = be.prefill_varlen(qd, kd, vd, cu_seqlens=cu, max_seqlen=ms)
+        torch.cuda.synchronize()
+        assert torch.equal(again, first)
+    stream = torch.cuda.Stream()
+    outs = []
+    with torch.cuda.stream(stream):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for _ in range(2):
+                outs.append(be.prefill_varlen(qd, kd, vd, cu_seqlens=cu, max_seqlen=ms))
+    for _ in range(3):
+        for o in outs:
+            o.zero_()
+        with torch.cuda.stream(stream):
+            graph.replay()
+        torch.cuda.synchronize()
+        assert all(torch.equal(o, first) for o in outs)
