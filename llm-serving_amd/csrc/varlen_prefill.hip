@@ -1365,6 +1365,13 @@ struct Duo {
   }
 };
 
+// 16-byte global store with the nontemporal (streaming) hint.
+__device__ __forceinline__ void store16_nt(void* p, const uint4& v) {
+  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 w = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(p));
+}
+
 // s_waitcnt lgkmcnt(0) alone (vmcnt and expcnt left at their maximum).
 __device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14)); }
 
@@ -1448,14 +1455,32 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
   auto seg_of = [&](const T* base, const Item& it) {
     return reinterpret_cast<const char*>(base) + int64_t(it.seq0) * kv_row_b + (it.h / G) * ROWB;
   };
-  uint4 qB[KS];
-  auto load_q = [&](const Item& it) {
-    const int qi = it.row0 + qb * 32 + col;
-    const int qc = qi < it.L ? qi : it.L - 1;
-    const T* qp_ = q + int64_t(it.seq0 + qc) * q_row + it.h * D + g * 8;
+  // An item's Q tile goes into LDS like a K tile (same swizzled rows, whole 16-byte chunks
+  // along each row, each row loaded once per workgroup), into V buffer 1, which is idle
+  // from the end of an item's fold until the next item's second step; rows past the
+  // segment read as zero. Its operand reads are the K reads shifted by (qb - kh) x 32 rows
+  // (sw(r) depends on r mod 32 only).
+  // The lane offsets are rebuilt per call from an opaque copy of the lane id (kept live
+  // through the item loop they would be spilled).
+  const int64_t q_row_b = q_row * int64_t(sizeof(T));
+  auto issue_q = [&](const Item& it) {
+    int ql = lane;
+    asm volatile("" : "+v"(ql));
+    const int qr0 = wave * W::RPS + ql / W::NCH;
+    const int qdma_off = int(qr0 * q_row_b) + (((ql % W::NCH) ^ W::sw(qr0)) << 4);
+    const int qdma_step = int(W::WAVES * W::RPS * q_row_b);
+    const int rows = min(it.L - it.row0, BQ);
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(reinterpret_cast<const char*>(q) + int64_t(it.seq0 + it.row0) * q_row_b + it.h * ROWB),
+        (short)0, rows * int(q_row_b), 0x00020000);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qB[ks] = load16(qp_ + ks * 16);
+    for (int i = 0; i < LPW; ++i) {
+      buffer_load_lds16(rs, (lds_void_t*)((__attribute__((address_space(3))) uint8_t*)vb1 + (wave + i * W::WAVES) * 1024),
+                        qdma_off + i * qdma_step);
+    }
   };
+  static_assert(BQ == BK, "a Q tile has the layout of a K tile");
+  uint4 qB[KS];
 
   // LDS byte offsets of this lane's operands within a buffer (as in the ring kernel): K
   // fragment of k-step ks, and the two transposed reads of each V^T operand (the second
@@ -1483,7 +1508,7 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
   Item it = decode();
   const char* kseg = seg_of(k, it);
   const char* vseg = seg_of(v, it);
-  load_q(it);
+  issue_q(it);
   issue(kseg, it, it.t_first, kb0);
   issue(kseg, it, it.t_first + 1, kb1);
 
@@ -1497,6 +1522,9 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
     bare_barrier();
     floatx16 cur;
     {
+      const uint8_t* qbuf = vb1 + (qb - kh) * 32 * ROWB;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) qB[ks] = *reinterpret_cast<const uint4*>(qbuf + k_rd[ks]);
       uint4 kf[KS];
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) kf[ks] = *reinterpret_cast<const uint4*>(kb0 + k_rd[ks]);
@@ -1505,7 +1533,7 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
       for (int ks = 0; ks < KS; ++ks) cur = mfma32<T>(kf[ks], qB[ks], cur);
     }
     wait_lgkm0();
-    bare_barrier();  // every wave has read K(t0) before step 0 refills its buffer
+    bare_barrier();  // every wave has read K(t0) before step 0 refills its buffer (and Q before step 1)
 
     floatx16 o[DB];
 #pragma unroll
@@ -1633,8 +1661,8 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
       drain(vb0);
     }
 
-    // the next item's first two K tiles, in flight during this item's epilogue (its Q goes
-    // into the registers once the fold has released them)
+    // the next item's first two K tiles, in flight during this item's epilogue (its Q tile
+    // follows once the fold has released V buffer 1)
     const Item cur_it = it;
     const bool more = idx + 1 < count;
     if (more) {
@@ -1659,7 +1687,6 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
     int ln = lane;
     asm volatile("" : "+v"(ln));
     const int e_col = ln & 31, e_g = ln >> 5;
-    const int e_qi = cur_it.row0 + qb * 32 + e_col;
     const float l_tot = l_i + swap32(l_i);
     mlx[kh][qb][0][ln] = m_i;
     mlx[kh][qb][1][ln] = l_tot;
@@ -1685,13 +1712,31 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
       const float w_o = fast_exp2(m_o - M_use);
       const float l_all = fmaf(l_o, w_o, l_tot * w_me);
       const float inv = 1.0f / fmaxf(l_all, 1e-30f);
+      // The normalised output goes out through LDS: the first 32 x HB * 64 bytes of this
+      // wave's kept blocks in fbuf (read just above, by this wave only) take it as
+      // [query row][HB * 32 dims] bf16 with 16-byte chunk c of row r at c ^ (r % NC), and
+      // are read back 16 bytes per lane along the row, so each global store writes whole
+      // 128-byte lines (stored straight from the MFMA layout, every lane's 8 bytes would
+      // touch another row: 32 lines per instruction). The stores carry the nontemporal
+      // hint: the output is not read again here, and in the XCD's L2 it would displace the
+      // K and V that the following items re-read.
+      constexpr int NC = HB * 4;  // 16-byte chunks of a staged row
+      uint8_t* stg = fbuf_bytes + KH * HB * 16 * 64 * 4;
 #pragma unroll
       for (int hb = 0; hb < HB; ++hb) {
         const int db = KH * HB + hb;
         float r[16];
 #pragma unroll
         for (int e = 0; e < 16; ++e) r[e] = fmaf(fbuf[(db * 16 + e) * 64 + ln], w_o, o[db][e] * w_me);
-        if (cur_it.n_split > 1) {
+        if (cur_it.n_split <= 1) {
+#pragma unroll
+          for (int jg = 0; jg < 4; ++jg) {
+            const uint2 val = make_uint2(pack2<T>(r[jg * 4 + 0] * inv, r[jg * 4 + 1] * inv),
+                                         pack2<T>(r[jg * 4 + 2] * inv, r[jg * 4 + 3] * inv));
+            const int pos = (hb * 4 + jg) ^ (e_col & (NC - 1));
+            *reinterpret_cast<uint2*>(stg + e_col * (NC * 16) + pos * 16 + e_g * 8) = val;
+          }
+        } else {
           // this piece's (O relative to M, M, l) for the merge launch; rows past the segment
           // are written too and never read
           float* pbase = partials + (int64_t(cur_it.slot + cur_it.split) * H + cur_it.h) * (BQ * (D + 2));
@@ -1703,16 +1748,18 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
                 make_float4(r[jg * 4 + 0], r[jg * 4 + 1], r[jg * 4 + 2], r[jg * 4 + 3]);
           }
           if (KH == 0 && hb == 0 && e_g == 0) *reinterpret_cast<float2*>(pbase + BQ * D + row * 2) = make_float2(M, l_all);
-          continue;
         }
-        if (e_qi < cur_it.L) {
-          T* op = out + int64_t(cur_it.seq0 + e_qi) * q_row + cur_it.h * D;
+      }
+      if (cur_it.n_split <= 1) {
+        // NC lanes per staged row, 64 / NC rows per wave-wide store
+        const int c = ln & (NC - 1);
 #pragma unroll
-          for (int jg = 0; jg < 4; ++jg) {
-            const int d = db * 32 + jg * 8 + e_g * 4;
-            const uint2 val = make_uint2(pack2<T>(r[jg * 4 + 0] * inv, r[jg * 4 + 1] * inv),
-                                         pack2<T>(r[jg * 4 + 2] * inv, r[jg * 4 + 3] * inv));
-            *reinterpret_cast<uint2*>(op + d) = val;
+        for (int i = 0; i < NC / 2; ++i) {
+          const int rr = i * (64 / NC) + ln / NC;
+          const uint4 val = *reinterpret_cast<const uint4*>(stg + rr * (NC * 16) + ((c ^ (rr & (NC - 1))) << 4));
+          const int qrow = cur_it.row0 + qb * 32 + rr;
+          if (qrow < cur_it.L) {
+            store16_nt(out + int64_t(cur_it.seq0 + qrow) * q_row + cur_it.h * D + KH * HB * 32 + c * 8, val);
           }
         }
       }
@@ -1724,9 +1771,9 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
     } else {
       if (kh == 0) fold_out(vb1, K0{}); else fold_out(vb1, K1{});
     }
-    if (more) load_q(it);
     wait_lgkm0();
     bare_barrier();  // the V ring and mlx are read before the next item refills them
+    if (more) issue_q(it);
   }
 }
 
