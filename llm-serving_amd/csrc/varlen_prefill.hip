@@ -1503,7 +1503,8 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
   }
   static_assert(W::sw(16) == W::sw(0) && W::sw(17) == W::sw(1), "16-row shift keeps the swizzle");
 
-  // first item: Q and K(t0), K(t0+1) in flight (later items get them from the epilogue)
+  // first item: Q, K(t0), K(t0+1) and V(t0) in flight (later items get them from the
+  // previous item's epilogue)
   load_words(0);
   Item it = decode();
   const char* kseg = seg_of(k, it);
@@ -1511,6 +1512,7 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
   issue_q(it);
   issue(kseg, it, it.t_first, kb0);
   issue(kseg, it, it.t_first + 1, kb1);
+  issue(vseg, it, it.t_first, vb0);
 
   for (int idx = 0; idx < count; ++idx) {
     const int L = it.L;
@@ -1560,14 +1562,15 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
     // scores of tile t+1 (K(t+1) in kb_next) and PV of tile t-1 (V(t-1) in vb_prev, P(t-1)
     // from the previous step), so every MFMA of the step is independent of the step's
     // softmax; K(t+2) goes to kb_free (K(t)'s buffer) and V(t) to vb_free (V(t-2)'s). The
-    // first step of an item has no PV (kPV false). Every step runs the masked softmax: an
+    // first step of an item has no PV (kPV false) and issues no V: V(t0) was issued into
+    // V buffer 0 together with the item's Q. Every step runs the masked softmax: an
     // unmasked copy for interior tiles pushes the kernel past its 256 registers.
     auto step = [&](int sidx, uint8_t* kb_next, uint8_t* kb_free, const uint8_t* vb_prev, uint8_t* vb_free,
                     auto pv_c) {
       constexpr bool kPV = decltype(pv_c)::value;
       const int t = it.t_first + sidx;
       issue(kseg, it, t + 2, kb_free);
-      issue(vseg, it, t, vb_free);
+      if constexpr (kPV) issue(vseg, it, t, vb_free);  // V(t0) came with the item's Q
       uint4 kf[KS];
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) kf[ks] = *reinterpret_cast<const uint4*>(kb_next + k_rd[ks]);
@@ -1773,7 +1776,10 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
     }
     wait_lgkm0();
     bare_barrier();  // the V ring and mlx are read before the next item refills them
-    if (more) issue_q(it);
+    if (more) {
+      issue_q(it);
+      issue(vseg, it, it.t_first, vb0);
+    }
   }
 }
 
