@@ -107,7 +107,7 @@ int mi_paged_decode(const void* q, const void* k_cache, const void* v_cache,
  * mi_varlen_schedule (host only) cuts the packed batch into query tiles, splits the
  * longest causal tiles' key ranges into pieces when the launch underfills the chip, and
  * orders the pieces heaviest-first so the causal triangle does not leave a tail of long
- * tiles. By default head_dim 64/128 batches whose longest segment reaches 2048 tokens run
+ * tiles. By default head_dim 64/128 batches whose longest segment reaches 8192 tokens run
  * the LDS-ring kernel (128-row tiles), shorter ones the persistent duo kernel (64-row
  * tiles, two workgroups per CU, each working through its own item list), head_dim 256 the
  * register-staged kernel (64-row tiles); mi_varlen_schedule_for names the kernel instead

@@ -49,10 +49,11 @@ constexpr int kXcds = 8; // MI355X: 8 XCDs, workgroups dispatched round-robin ov
 // register-staged kernel.
 constexpr int kSchedHeader = 4;
 // The ring kernel is chosen when the longest segment reaches this many tokens: measured on
-// MI355X (H16/H_kv8/D128 bf16) it is 23% faster on one 4096-token segment, and 7-19%
-// slower on batches of segments up to ~1.7K tokens, where the register-staged kernel's
-// two workgroups per CU overlap each other's start-up and barrier phases.
-constexpr int kRingMinLen = 2048;
+// MI355X (H16/H_kv8/D128 bf16, causal) the duo kernel is faster up to 6144 tokens (30.0
+// against 39.3 us at 2048, 84.4 against 87.0 us at 4096, 187 against 195 us at 6144, and
+// 42.0 against 31.7 us on the config-3 batch); the ring kernel's 128-row tiles are 2%
+// faster at 8192 and 4% at 16384 tokens.
+constexpr int kRingMinLen = 8192;
 #ifndef MIATTN_PREFILL_SPLIT
 #define MIATTN_PREFILL_SPLIT 1
 #endif

@@ -51,9 +51,9 @@ PER_CU = {0: 2, 1: 1, 2: 1, 3: 2}      # workgroups one CU runs at once
 
 
 def _kind(kernel, D, lengths=()):
-    if kernel is None:  # head_dim 64/128: ring from a 2048-token segment, duo below; staged otherwise
+    if kernel is None:  # head_dim 64/128: ring from an 8192-token segment, duo below; staged otherwise
         if D in (64, 128):
-            return 1 if max(lengths) >= 2048 else 3
+            return 1 if max(lengths) >= 8192 else 3
         return 0
     return KERNELS[kernel]
 
@@ -141,10 +141,12 @@ def _piece_work(lengths, p, kind):
 
 
 @pytest.mark.parametrize("lengths,H,kernel", [
-    ([100, 1, 700, 64, 65, 1742, 450], 16, None),     # duo kernel (< 2048 tokens), fills the chip
+    ([100, 1, 700, 64, 65, 1742, 450], 16, None),     # duo kernel (< 8192 tokens), fills the chip
     ([100, 1, 700, 64, 65, 1742, 450], 16, "staged"),
     ([100, 1, 700, 64, 65, 1742, 450], 16, "wide"),   # fills the chip: not split
-    ([100, 1, 2100, 64, 65], 4, None),                # ring kernel, underfilled: split pieces
+    ([100, 1, 2100, 64, 65], 4, "ring"),              # underfilled: split pieces
+    ([100, 8200], 2, None),                           # ring kernel (>= 8192 tokens), underfilled
+    ([100, 1, 2100, 64, 65], 4, None),                # duo kernel, underfilled: split pieces
     ([100, 1, 2100, 64, 65], 2, "wide"),
     ([100, 1, 2100, 64, 65], 4, "duo"),
 ])
