@@ -1940,10 +1940,12 @@ struct Piece { int work, w0, w1; };
 // the least work so far (LPT); when the KV heads divide evenly over the XCDs, the items of
 // a KV head go to the workgroups of one XCD (workgroup w runs on XCD w % kXcds), so its K
 // and V stay in that XCD's L2. An item costs its key tiles plus kItemOverhead for its
-// prologue and epilogue.
+// prologue and epilogue: a workgroup's extra single-tile item takes about as long as five
+// 64-key steps, and counting 8 balances best (config-3 batch 31.5 us against 32.2 us with
+// 3, 31.8 with 12, 32.9 with 16; batches of equal or mid-length segments unchanged).
 int duo_schedule(const int32_t* cu, const std::vector<Piece>& pieces, const std::vector<Piece>& merges,
                  int n_partials, int H, int H_kv, int D, int32_t* out, int capacity) {
-  constexpr int kCUs = 256, kSlots = 2 * kCUs, kItemOverhead = 3;
+  constexpr int kCUs = 256, kSlots = 2 * kCUs, kItemOverhead = 8;
   const int64_t n_items = int64_t(pieces.size()) * H;
   const int n_wg = int(std::min<int64_t>(kSlots, n_items));
   const int n_merge = int(merges.size());
