@@ -1572,6 +1572,10 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
       const int t = it.t_first + sidx;
       issue(kseg, it, t + 2, kb_free);
       if constexpr (kPV) issue(vseg, it, t, vb_free);  // V(t0) came with the item's Q
+      // Higher wave priority from here to the end-of-step wait: when the two waves sharing a
+      // SIMD (one per workgroup) both have work, the one in its MFMA/softmax section issues
+      // first, which keeps the matrix pipe fed (3-4% faster than equal priorities).
+      __builtin_amdgcn_s_setprio(1);
       uint4 kf[KS];
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) kf[ks] = *reinterpret_cast<const uint4*>(kb_next + k_rd[ks]);
@@ -1637,6 +1641,7 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
                             pack2<T>(sc[8 * t2 + 4], sc[8 * t2 + 5]), pack2<T>(sc[8 * t2 + 6], sc[8 * t2 + 7]));
       }
       cur = nxt;
+      __builtin_amdgcn_s_setprio(0);
       wait_vm_lgkm0<0>();
       bare_barrier();
     };
