@@ -11,6 +11,9 @@
  *                                              kernel :545-643)
  *   mi_varlen_prefill  packed varlen causal    replaces FlashVarlen.prefill_varlen
  *                      prefill attention       (reference model/attention/varlen.py:317-357)
+ *   mi_qk_norm_rope_write  decode-step         fuses q_norm/k_norm + apply_rotary_emb +
+ *                      attention epilogue      PagedKV.write (reference model/layers.py:193-211,
+ *                                              :342-350, :59-89; model/paged.py:503-520)
  *
  * Conventions shared by every entry point:
  *   - every pointer except the `host_*` arguments is a device pointer;
@@ -67,6 +70,27 @@ int mi_kv_slot_write(const void* k, const void* v, const void* slot_ids, int slo
                      void* k_pool, void* v_pool, int64_t n_tokens, int H_kv, int D,
                      int64_t n_slots, const int64_t* src_strides, int dtype,
                      int32_t* error_word, void* stream);
+
+/* ------------------------------------------------------------------ decode-step epilogue
+ * One decode step's attention epilogue of one layer, fused (the reference runs it as tensor
+ * ops: q_norm / k_norm = RMSNorm, model/layers.py:342-350 at :193-194; apply_rotary_emb,
+ * :59-89 at :210-211; then PagedKV.write, model/paged.py:503-520). For each row b of the
+ * packed projection output qkv (B rows of row_stride elements, each [q (H x D) | k (H_kv
+ * x D) | v (H_kv x D)]):
+ *     q_out[b, h]           = rope(rmsnorm(q[b, h], q_norm_w), pos[b])       (B, H, D) contiguous
+ *     k_pool_flat[slot[b]]  = rope(rmsnorm(k[b, :], k_norm_w), pos[b])
+ *     v_pool_flat[slot[b]]  = v[b, :]
+ * rmsnorm(x, w) = x / sqrt(mean(x^2) + eps) * w and NeoX rope with the (n_pos, D/2) cos/sin
+ * tables at row pos[b] (int64), computed with the reference's per-op rounding to the
+ * activation dtype (see csrc/decode_epilogue.hip). slot_ids as for mi_kv_slot_write (int32 or
+ * int64 per slot_bits; pools (n_slots, H_kv, D) contiguous). A row whose position is outside
+ * [0, n_pos) or whose slot is outside [0, n_slots) is not written and 1 + its index goes to
+ * *error_word (may be NULL). D = 64, 128 or 256. */
+int mi_qk_norm_rope_write(const void* qkv, int64_t row_stride, const void* q_norm_w,
+                          const void* k_norm_w, const void* cos_tab, const void* sin_tab,
+                          int64_t n_pos, const int64_t* pos, const void* slot_ids, int slot_bits,
+                          void* q_out, void* k_pool, void* v_pool, int B, int H, int H_kv, int D,
+                          int64_t n_slots, float eps, int dtype, int32_t* error_word, void* stream);
 
 /* ------------------------------------------------------------------ paged decode
  * Replaces paged_decode (reference model/triton_decode.py:250-328) and its kernel

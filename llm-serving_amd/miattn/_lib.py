@@ -72,6 +72,12 @@ SIGNATURES: dict[str, tuple] = {
         _c_int, [_p_int32, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _p_int32, _c_int]
     ),
     "mi_varlen_workspace_size": (_c_size_t, [_p_int32, _c_int]),
+    "mi_qk_norm_rope_write": (
+        _c_int,
+        [_c_void_p, _c_int64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int64, _c_void_p,
+         _c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int,
+         _c_int64, _c_float, _c_int, _c_void_p, _c_void_p],
+    ),
     "mi_varlen_prefill": (
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
@@ -80,7 +86,7 @@ SIGNATURES: dict[str, tuple] = {
     ),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 
 def _load():

@@ -36,7 +36,7 @@ HIPCC_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
-SOURCES = ["capi.hip", "slot_write.hip", "paged_decode.hip", "varlen_prefill.hip"]
+SOURCES = ["capi.hip", "slot_write.hip", "paged_decode.hip", "varlen_prefill.hip", "decode_epilogue.hip"]
 
 
 def _hipcc() -> str:

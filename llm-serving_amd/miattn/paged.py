@@ -172,6 +172,62 @@ class PagedPool:
         if self.strict_writes:
             self.check_writes()
 
+    def write_qk_norm_rope(self, layer: int, slot_ids: torch.Tensor, qkv: torch.Tensor,
+                           q_norm_w: torch.Tensor, k_norm_w: torch.Tensor, cos: torch.Tensor,
+                           sin: torch.Tensor, pos: torch.Tensor, eps: float) -> torch.Tensor:
+        """One decode step's attention epilogue in one HIP launch: per-head RMSNorm of q and k
+        (weights ``q_norm_w``/``k_norm_w``, ``(head_dim,)``), NeoX RoPE at ``pos`` (int64,
+        one per row) from the ``(n_pos, head_dim/2)`` ``cos``/``sin`` tables, k and v written
+        at ``slot_ids``; returns q ``(B, n_head, head_dim)``, contiguous for the paged decode.
+
+        ``qkv`` is the packed projection output ``(B, (n_head + 2 * n_kv_head) * head_dim)``
+        (rows ``[q | k | v]``, unit element stride). The reference runs this as tensor ops
+        (``model/layers.py:193-211``: q_norm/k_norm, ``apply_rotary_emb``) followed by
+        ``PagedKV.write`` (``model/paged.py:503-520``); the kernel rounds each step to the
+        pool dtype as those ops do. A row whose position is outside the tables or whose slot
+        is outside the pool is not written and is reported by :meth:`check_writes`.
+        """
+        layer = self._check_layer(layer)
+        H, H_kv, D = self.n_head, self.n_kv_head, self.head_dim
+        if qkv.dim() != 2 or qkv.shape[1] != (H + 2 * H_kv) * D or qkv.stride(1) != 1:
+            raise ValueError(
+                f"qkv must be (B, {(H + 2 * H_kv) * D}) with unit element stride, got {tuple(qkv.shape)} "
+                f"strides {tuple(qkv.stride())}"
+            )
+        B = int(qkv.shape[0])
+        for name, t, shape in (("q_norm_w", q_norm_w, (D,)), ("k_norm_w", k_norm_w, (D,))):
+            if tuple(t.shape) != shape or not t.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous ({D},) tensor, got {tuple(t.shape)}")
+        if cos.dim() != 2 or cos.shape[1] != D // 2 or tuple(sin.shape) != tuple(cos.shape):
+            raise ValueError(f"cos/sin must be (n_pos, {D // 2}), got {tuple(cos.shape)} / {tuple(sin.shape)}")
+        if not (cos.is_contiguous() and sin.is_contiguous()):
+            raise ValueError("cos/sin tables must be contiguous")
+        if pos.dim() != 1 or pos.numel() != B or pos.dtype != torch.int64:
+            raise ValueError(f"pos must be an int64 tensor of {B} positions, got {pos.dtype} {tuple(pos.shape)}")
+        if slot_ids.dim() != 1 or slot_ids.numel() != B or slot_ids.dtype not in (torch.int32, torch.int64):
+            raise ValueError(f"slot_ids must be {B} int32/int64 slots, got {slot_ids.dtype} {tuple(slot_ids.shape)}")
+        for name, t in (("qkv", qkv), ("q_norm_w", q_norm_w), ("k_norm_w", k_norm_w), ("cos", cos), ("sin", sin)):
+            if t.dtype != self.dtype:
+                raise ValueError(f"{name} is {t.dtype}, the pool holds {self.dtype}")
+        _lib.require_library("PagedPool.write_qk_norm_rope")
+        tensors = (qkv, q_norm_w, k_norm_w, cos, sin, pos, slot_ids)
+        if self.device.type != "cuda" or not all(t.is_cuda for t in tensors):
+            raise RuntimeError("PagedPool.write_qk_norm_rope is a HIP kernel and needs CUDA (HIP) tensors")
+        slot_ids = slot_ids.contiguous()
+        pos = pos.contiguous()
+        q = torch.empty((B, H, D), dtype=self.dtype, device=self.device)
+        rc = _lib.lib.mi_qk_norm_rope_write(
+            qkv.data_ptr(), qkv.stride(0), q_norm_w.data_ptr(), k_norm_w.data_ptr(), cos.data_ptr(),
+            sin.data_ptr(), cos.shape[0], pos.data_ptr(), slot_ids.data_ptr(),
+            32 if slot_ids.dtype == torch.int32 else 64, q.data_ptr(), self.keys[layer].data_ptr(),
+            self.values[layer].data_ptr(), B, H, H_kv, D, self.n_slots, float(eps),
+            _lib.dtype_code(self.dtype), self._write_error.data_ptr(), _lib.current_stream(qkv.device),
+        )
+        _lib.check(rc, "PagedPool.write_qk_norm_rope")
+        if self.strict_writes:
+            self.check_writes()
+        return q
+
     def check_writes(self) -> None:
         """Raise ``IndexError`` if a write since the last check met an out-of-range slot.
 
@@ -355,6 +411,23 @@ class PagedKV:
             )
         self.pool.write_slots(layer, self._slot_ids, k[:, :, 0, :], v[:, :, 0, :])
         self._step_written = True
+
+    def write_rope(self, layer: int, qkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: torch.Tensor,
+                   cos: torch.Tensor, sin: torch.Tensor, eps: float) -> torch.Tensor:
+        """This step's q/k RMSNorm + RoPE (at each row's position) and K/V write in one HIP
+        launch (:meth:`PagedPool.write_qk_norm_rope`, in place of the reference's tensor ops
+        and :meth:`write`); ``qkv`` is the packed projection ``(B, (H + 2 H_kv) D)``. Returns
+        q ``(B, n_head, 1, head_dim)`` for :meth:`attend`."""
+        if self.check_bounds and max(self._host_pos) >= self.max_len:
+            raise IndexError(f"PagedKV overflow: write position {max(self._host_pos)} >= max_len {self.max_len}")
+        if self._slot_ids is None:
+            row, position, block_index, have = self._slot_error or (-1, -1, -1, -1)
+            raise IndexError(
+                f"row {row}: position {position} needs block {block_index}, but its block table has {have} blocks"
+            )
+        q = self.pool.write_qk_norm_rope(layer, self._slot_ids, qkv, q_norm_w, k_norm_w, cos, sin, self.pos, eps)
+        self._step_written = True
+        return q.unsqueeze(2)
 
     def attend(self, layer: int, q: torch.Tensor, *, dropout_p: float = 0.0) -> torch.Tensor:
         """Block-table decode of one layer; ``q`` ``(B, H, 1, D)`` -> same shape

@@ -7,7 +7,10 @@ bf16 weights drawn N(0, 0.02). Only the attention path is this package's: packed
 goes through :class:`~miattn.packed.PackedPrefill` (HIP varlen kernel + one slot-write
 launch per layer) and decode through :class:`~miattn.paged.PagedKV` (HIP slot write +
 block-table decode), exactly the containers the reference's layers call
-(reference ``model/layers.py:217-250``). Projections, norms and RoPE are plain torch.
+(reference ``model/layers.py:217-250``). Projections and the residual-stream norms are
+plain torch; in decode, the q/k norms, RoPE and the K/V write run as one HIP launch per
+layer (``PagedPool.write_qk_norm_rope``) over one projection GEMM of the stacked q/k/v
+weights, with the reference ops' rounding (prefill keeps the tensor ops).
 
 :class:`GraphDecoder` is the decode step with no host work per step: slot map, seqlen,
 RoPE rows, 28 layers, lm_head and the greedy argmax are captured once in a HIP graph and
@@ -104,6 +107,11 @@ class Qwen3:
         self.cfg = cfg
         self.device = torch.device(device)
         self.w = {k: v.to(self.device) for k, v in weights.items()}
+        # decode projects q, k and v with one GEMM over the stacked weights (the same dot
+        # products as three separate projections); its output rows are [q | k | v]
+        for i in range(cfg.n_layer):
+            p = f"l{i}."
+            self.w[p + "wqkv"] = torch.cat([self.w[p + "wq"], self.w[p + "wk"], self.w[p + "wv"]], 0).contiguous()
         self.dtype = self.w["embed"].dtype
         self.cos, self.sin = rope_table(cfg.head_dim, cfg.rope_theta, max_pos, self.device, self.dtype)
 
@@ -160,14 +168,15 @@ class Qwen3:
         branch, ``model/minillm.py:111-136``); returns logits ``(B, vocab)``."""
         c = self.cfg
         paged.build_mask(next_token=True)
-        cos, sin = self.cos[paged.pos].unsqueeze(1), self.sin[paged.pos].unsqueeze(1)  # (B, 1, D/2)
         x = F.embedding(tokens.view(-1, 1), self.w["embed"])  # (B, 1, C)
+        B = x.shape[0]
         for i in range(c.n_layer):
-            h = rms_norm(x, self.w[f"l{i}.ln1"], c.eps)
-            q, k, v = self._qkv(i, h)  # (B, 1, H, D)
-            q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
-            paged.write(i, k.permute(0, 2, 1, 3), v.permute(0, 2, 1, 3))
-            y = paged.attend(i, q.transpose(1, 2))  # (B, H, 1, D)
+            p = f"l{i}."
+            h = rms_norm(x, self.w[p + "ln1"], c.eps)
+            qkv = F.linear(h, self.w[p + "wqkv"]).view(B, -1)
+            # q/k norm + RoPE + K/V write in one HIP launch (the reference's tensor ops + write)
+            q = paged.write_rope(i, qkv, self.w[p + "qn"], self.w[p + "kn"], self.cos, self.sin, c.eps)
+            y = paged.attend(i, q)  # (B, H, 1, D)
             x = x + F.linear(y.transpose(1, 2).reshape(x.shape[0], 1, -1), self.w[f"l{i}.wo"])
             x = x + self._mlp(i, rms_norm(x, self.w[f"l{i}.ln2"], c.eps))
         paged.advance()
@@ -215,14 +224,14 @@ class GraphDecoder:
         m, c, bs = self.model, self.model.cfg, self.pool.block_size
         self.seqlen.copy_((self.pos + 1).to(torch.int32))
         slots = self.table64.gather(1, (self.pos // bs).view(-1, 1)).view(-1) * bs + self.pos % bs
-        cos, sin = m.cos[self.pos].unsqueeze(1), m.sin[self.pos].unsqueeze(1)
         x = F.embedding(self.tokens.view(-1, 1), m.w["embed"])
         for i in range(c.n_layer):
-            h = rms_norm(x, m.w[f"l{i}.ln1"], c.eps)
-            q, k, v = m._qkv(i, h)
-            q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
-            self.pool.write_slots(i, slots, k[:, 0], v[:, 0])
-            y = self.plan.run(i, q[:, 0].contiguous())  # (B, H, D)
+            p = f"l{i}."
+            h = rms_norm(x, m.w[p + "ln1"], c.eps)
+            qkv = F.linear(h, m.w[p + "wqkv"]).view(self.B, -1)
+            q = self.pool.write_qk_norm_rope(i, slots, qkv, m.w[p + "qn"], m.w[p + "kn"], m.cos, m.sin,
+                                             self.pos, c.eps)
+            y = self.plan.run(i, q)  # (B, H, D)
             x = x + F.linear(y.reshape(self.B, 1, -1), m.w[f"l{i}.wo"])
             x = x + m._mlp(i, rms_norm(x, m.w[f"l{i}.ln2"], c.eps))
         nxt = m.logits(x[:, 0]).argmax(-1)

@@ -1,0 +1,101 @@
+"""The fused decode-step epilogue (q/k RMSNorm + RoPE + paged K/V write, one HIP launch)
+against the reference's tensor-op chain run on the same device.
+
+The chain is the reference's (``model/layers.py:342-350`` RMSNorm, ``:59-89``
+``apply_rotary_emb``, ``model/paged.py:503-520`` the write), restated by
+``miattn.qwen3.rms_norm`` / ``apply_rope`` and ``PagedPool.write_slots``. The kernel rounds
+each step to the activation dtype as those ops do, so outputs are equal except where the
+fp32 sum of squares, accumulated in another order than torch's reduction, crosses a
+rounding boundary of the mean: a few elements may then differ by one or two ulps (1/128
+relative in bf16). V is a copy: bit-exact.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from miattn import PagedPool
+from miattn.qwen3 import apply_rope, rms_norm, rope_table
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(B, H, H_kv, D, dtype, seed, n_blocks=64, bs=16, n_pos=4096, slot_dtype=torch.int64):
+    g = torch.Generator().manual_seed(seed)
+    qkv = (torch.randn(B, (H + 2 * H_kv) * D, generator=g) * 2.0).to(dtype).cuda()
+    qn = (1.0 + 0.1 * torch.randn(D, generator=g)).to(dtype).cuda()
+    kn = (1.0 + 0.1 * torch.randn(D, generator=g)).to(dtype).cuda()
+    cos, sin = rope_table(D, 1e6, n_pos, "cuda", dtype)
+    pos = torch.randint(0, n_pos, (B,), generator=g).cuda()
+    slots = torch.randperm(n_blocks * bs, generator=g)[:B].to(slot_dtype).cuda()
+    return qkv, qn, kn, cos, sin, pos, slots
+
+
+def _reference(pool_ref, layer, qkv, qn, kn, cos, sin, pos, slots, H, H_kv, D, eps):
+    B = qkv.shape[0]
+    q = qkv[:, : H * D].view(B, 1, H, D)
+    k = qkv[:, H * D:(H + H_kv) * D].view(B, 1, H_kv, D)
+    v = qkv[:, (H + H_kv) * D:].view(B, 1, H_kv, D)
+    q, k = rms_norm(q, qn, eps), rms_norm(k, kn, eps)
+    c, s = cos[pos].unsqueeze(1), sin[pos].unsqueeze(1)
+    q, k = apply_rope(q, c, s), apply_rope(k, c, s)
+    pool_ref.write_slots(layer, slots, k[:, 0], v[:, 0])
+    return q[:, 0]
+
+
+def _ulps(a, b, dtype):
+    # distance in units of the dtype's last place at b's magnitude
+    eps = torch.finfo(dtype).eps
+    scale = torch.clamp(b.float().abs(), min=torch.finfo(dtype).tiny)
+    return ((a.float() - b.float()).abs() / (scale * eps)).max().item()
+
+
+@pytest.mark.parametrize("B,H,H_kv,D", [(32, 16, 8, 128), (5, 8, 2, 256), (7, 4, 4, 64), (1, 16, 8, 128)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("slot_dtype", [torch.int64, torch.int32])
+def test_epilogue_matches_the_reference_op_chain(B, H, H_kv, D, dtype, slot_dtype):
+    eps = 1e-6
+    qkv, qn, kn, cos, sin, pos, slots = _case(B, H, H_kv, D, dtype, seed=B * 7 + D, slot_dtype=slot_dtype)
+    pool = PagedPool(2, 64, 16, H_kv, D, dtype=dtype, device="cuda", n_head=H, strict_writes=True)
+    ref = PagedPool(2, 64, 16, H_kv, D, dtype=dtype, device="cuda", n_head=H, strict_writes=True)
+    q = pool.write_qk_norm_rope(1, slots, qkv, qn, kn, cos, sin, pos, eps)
+    q_ref = _reference(ref, 1, qkv, qn, kn, cos, sin, pos, slots, H, H_kv, D, eps)
+    torch.cuda.synchronize()
+    assert q.shape == (B, H, D) and q.is_contiguous()
+    assert torch.equal(pool.values[1], ref.values[1])  # v: a copy
+    assert torch.equal(pool.keys[0], ref.keys[0]) and torch.equal(pool.values[0], ref.values[0])  # other layer untouched
+    for got, want in ((q, q_ref), (pool.keys[1], ref.keys[1])):
+        same = (got == want).float().mean().item()
+        assert same > 0.999, f"only {same:.4%} of elements equal"
+        assert _ulps(got, want, dtype) <= 2.0
+
+
+def test_epilogue_rejects_bad_rows_without_writing():
+    H, H_kv, D, dtype = 16, 8, 128, torch.bfloat16
+    qkv, qn, kn, cos, sin, pos, slots = _case(4, H, H_kv, D, dtype, seed=3)
+    pool = PagedPool(1, 64, 16, H_kv, D, dtype=dtype, device="cuda", n_head=H)
+    slots[2] = pool.n_slots  # outside the pool
+    pool.write_qk_norm_rope(0, slots, qkv, qn, kn, cos, sin, pos, 1e-6)
+    with pytest.raises(IndexError):
+        pool.check_writes()
+    written = (pool.keys[0].view(pool.n_slots, -1) != 0).any(1)
+    assert written.sum().item() == 3 and not written[slots[[0, 1, 3]].cpu()].logical_not().any()
+    pos[1] = cos.shape[0]  # outside the RoPE table
+    slots[2] = 5
+    pool2 = PagedPool(1, 64, 16, H_kv, D, dtype=dtype, device="cuda", n_head=H)
+    pool2.write_qk_norm_rope(0, slots, qkv, qn, kn, cos, sin, pos, 1e-6)
+    with pytest.raises(IndexError):
+        pool2.check_writes()
+
+
+def test_epilogue_validates_shapes():
+    H, H_kv, D, dtype = 16, 8, 128, torch.bfloat16
+    qkv, qn, kn, cos, sin, pos, slots = _case(4, H, H_kv, D, dtype, seed=4)
+    pool = PagedPool(1, 64, 16, H_kv, D, dtype=dtype, device="cuda", n_head=H)
+    with pytest.raises(ValueError, match="qkv"):
+        pool.write_qk_norm_rope(0, slots, qkv[:, 1:], qn, kn, cos, sin, pos, 1e-6)
+    with pytest.raises(ValueError, match="pos"):
+        pool.write_qk_norm_rope(0, slots, qkv, qn, kn, cos, sin, pos.int(), 1e-6)
+    with pytest.raises(ValueError, match="cos/sin"):
+        pool.write_qk_norm_rope(0, slots, qkv, qn, kn, cos[:, 1:], sin[:, 1:], pos, 1e-6)
