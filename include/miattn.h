@@ -14,6 +14,9 @@
  *   mi_qk_norm_rope_write  decode-step         fuses q_norm/k_norm + apply_rotary_emb +
  *                      attention epilogue      PagedKV.write (reference model/layers.py:193-211,
  *                                              :342-350, :59-89; model/paged.py:503-520)
+ *   mi_add_rms_norm,   decode-step small ops   residual add + RMSNorm, SiLU(gate) * up
+ *   mi_silu_mul                                (reference model/layers.py:365-367, :342-350,
+ *                                              :325-335)
  *
  * Conventions shared by every entry point:
  *   - every pointer except the `host_*` arguments is a device pointer;
@@ -91,6 +94,20 @@ int mi_qk_norm_rope_write(const void* qkv, int64_t row_stride, const void* q_nor
                           int64_t n_pos, const int64_t* pos, const void* slot_ids, int slot_bits,
                           void* q_out, void* k_pool, void* v_pool, int B, int H, int H_kv, int D,
                           int64_t n_slots, float eps, int dtype, int32_t* error_word, void* stream);
+
+/* ------------------------------------------------------------------ decode-step small ops
+ * The residual stream's add + RMSNorm and the MLP's SiLU(gate) * up, each one launch (the
+ * reference runs them as tensor ops: block x = x + attn(norm1(x)); x = x + mlp(norm2(x)),
+ * model/layers.py:365-367; RMSNorm :342-350; MLP down(silu(gate(x)) * up(x)), :325-335),
+ * rounded op by op to the activation dtype like those ops (see csrc/decode_step.hip).
+ * mi_add_rms_norm: rows x cols contiguous; s = x + delta (delta may be NULL: s = x);
+ *   x_out = s (may be NULL, may alias x); h_out = s / sqrt(mean(s^2) + eps) * weight.
+ *   cols <= 4096.
+ * mi_silu_mul: gate_up (rows, 2 * inter) contiguous rows [gate | up];
+ *   out (rows, inter) = silu(gate) * up. */
+int mi_add_rms_norm(const void* x, const void* delta, const void* weight, void* x_out, void* h_out,
+                    int rows, int cols, float eps, int dtype, void* stream);
+int mi_silu_mul(const void* gate_up, void* out, int rows, int inter, int dtype, void* stream);
 
 /* ------------------------------------------------------------------ paged decode
  * Replaces paged_decode (reference model/triton_decode.py:250-328) and its kernel

@@ -72,6 +72,10 @@ SIGNATURES: dict[str, tuple] = {
         _c_int, [_p_int32, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _p_int32, _c_int]
     ),
     "mi_varlen_workspace_size": (_c_size_t, [_p_int32, _c_int]),
+    "mi_add_rms_norm": (
+        _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_float, _c_int, _c_void_p]
+    ),
+    "mi_silu_mul": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_void_p]),
     "mi_qk_norm_rope_write": (
         _c_int,
         [_c_void_p, _c_int64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int64, _c_void_p,
@@ -86,7 +90,7 @@ SIGNATURES: dict[str, tuple] = {
     ),
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 
 def _load():

@@ -36,7 +36,8 @@ HIPCC_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
-SOURCES = ["capi.hip", "slot_write.hip", "paged_decode.hip", "varlen_prefill.hip", "decode_epilogue.hip"]
+SOURCES = ["capi.hip", "slot_write.hip", "paged_decode.hip", "varlen_prefill.hip", "decode_epilogue.hip",
+           "decode_step.hip"]
 
 
 def _hipcc() -> str:

@@ -10,7 +10,9 @@ block-table decode), exactly the containers the reference's layers call
 (reference ``model/layers.py:217-250``). Projections and the residual-stream norms are
 plain torch; in decode, the q/k norms, RoPE and the K/V write run as one HIP launch per
 layer (``PagedPool.write_qk_norm_rope``) over one projection GEMM of the stacked q/k/v
-weights, with the reference ops' rounding (prefill keeps the tensor ops).
+weights, each residual add with the next RMSNorm is one launch (``add_rms_norm``) and the
+MLP's SiLU * up another (``silu_mul``), all with the reference ops' rounding (prefill keeps
+the tensor ops).
 
 :class:`GraphDecoder` is the decode step with no host work per step: slot map, seqlen,
 RoPE rows, 28 layers, lm_head and the greedy argmax are captured once in a HIP graph and
@@ -99,6 +101,37 @@ def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.T
     return torch.cat([x1 * cos - x2 * sin, x1 * sin + x2 * cos], dim=-1)
 
 
+def add_rms_norm(x: torch.Tensor, delta: torch.Tensor | None, weight: torch.Tensor, eps: float):
+    """``x + delta`` (in place into ``x``) and its RMSNorm in one HIP launch (``mi_add_rms_norm``),
+    rounded op by op as :func:`rms_norm` and the residual add are; returns ``(x, h)``.
+    ``x``/``delta``: contiguous ``(rows, cols)``; ``delta`` None normalises ``x`` as is."""
+    rows, cols = x.shape
+    for name, t in (("x", x), ("delta", delta)):
+        if t is not None and (not t.is_contiguous() or tuple(t.shape) != (rows, cols) or t.dtype != x.dtype):
+            raise ValueError(f"{name} must be contiguous ({rows}, {cols}) {x.dtype}, got {tuple(t.shape)} {t.dtype}")
+    if tuple(weight.shape) != (cols,) or weight.dtype != x.dtype:
+        raise ValueError(f"weight must be ({cols},) {x.dtype}")
+    h = torch.empty_like(x)
+    rc = _lib.lib.mi_add_rms_norm(x.data_ptr(), None if delta is None else delta.data_ptr(), weight.data_ptr(),
+                                  x.data_ptr() if delta is not None else None, h.data_ptr(), rows, cols, float(eps),
+                                  _lib.dtype_code(x.dtype), _lib.current_stream(x.device))
+    _lib.check(rc, "add_rms_norm")
+    return x, h
+
+
+def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
+    """``silu(gate) * up`` of a ``(rows, 2 * inter)`` ``[gate | up]`` projection in one HIP
+    launch (``mi_silu_mul``), rounded op by op as ``F.silu(g) * u`` is."""
+    rows, two = gate_up.shape
+    if two % 2 or not gate_up.is_contiguous():
+        raise ValueError(f"gate_up must be contiguous (rows, 2 * inter), got {tuple(gate_up.shape)}")
+    out = torch.empty((rows, two // 2), dtype=gate_up.dtype, device=gate_up.device)
+    rc = _lib.lib.mi_silu_mul(gate_up.data_ptr(), out.data_ptr(), rows, two // 2, _lib.dtype_code(gate_up.dtype),
+                              _lib.current_stream(gate_up.device))
+    _lib.check(rc, "silu_mul")
+    return out
+
+
 class Qwen3:
     """The model on one HIP device, attention through this package's containers."""
 
@@ -112,6 +145,7 @@ class Qwen3:
         for i in range(cfg.n_layer):
             p = f"l{i}."
             self.w[p + "wqkv"] = torch.cat([self.w[p + "wq"], self.w[p + "wk"], self.w[p + "wv"]], 0).contiguous()
+            self.w[p + "wgu"] = torch.cat([self.w[p + "wg"], self.w[p + "wu"]], 0).contiguous()
         self.dtype = self.w["embed"].dtype
         self.cos, self.sin = rope_table(cfg.head_dim, cfg.rope_theta, max_pos, self.device, self.dtype)
 
@@ -163,24 +197,41 @@ class Qwen3:
         return self.logits(x[0, packed.last_token_index])
 
     # ------------------------------------------------------------------ decode
+    def _decode_stack(self, x: torch.Tensor, attend) -> torch.Tensor:
+        """The 28 layers of a decode step on the ``(B, C)`` residual stream ``x`` (updated in
+        place): residual adds fused with the next RMSNorm (``add_rms_norm``), one GEMM for
+        q/k/v and one for gate/up, SiLU * up in one launch, and ``attend(i, qkv)`` giving
+        layer i's attention output ``(B, H * D)`` from its packed projection. Returns the
+        final RMSNorm of the stream (the lm_head input). Same arithmetic as the reference's
+        block (``model/layers.py:365-367``) op by op."""
+        c = self.cfg
+        _, h = add_rms_norm(x, None, self.w["l0.ln1"], c.eps)
+        for i in range(c.n_layer):
+            p = f"l{i}."
+            y = attend(i, F.linear(h, self.w[p + "wqkv"]))
+            _, h = add_rms_norm(x, F.linear(y, self.w[p + "wo"]), self.w[p + "ln2"], c.eps)
+            m = silu_mul(F.linear(h, self.w[p + "wgu"]))
+            nxt = self.w[f"l{i + 1}.ln1"] if i + 1 < c.n_layer else self.w["norm"]
+            _, h = add_rms_norm(x, F.linear(m, self.w[p + "wd"]), nxt, c.eps)
+        return h
+
     def decode(self, paged: PagedKV, tokens: torch.Tensor) -> torch.Tensor:
         """One decode step of every row (reference ``MiniLLM.forward`` decode-container
         branch, ``model/minillm.py:111-136``); returns logits ``(B, vocab)``."""
         c = self.cfg
         paged.build_mask(next_token=True)
-        x = F.embedding(tokens.view(-1, 1), self.w["embed"])  # (B, 1, C)
+        x = F.embedding(tokens.view(-1), self.w["embed"])  # (B, C)
         B = x.shape[0]
-        for i in range(c.n_layer):
-            p = f"l{i}."
-            h = rms_norm(x, self.w[p + "ln1"], c.eps)
-            qkv = F.linear(h, self.w[p + "wqkv"]).view(B, -1)
+
+        def attend(i: int, qkv: torch.Tensor) -> torch.Tensor:
             # q/k norm + RoPE + K/V write in one HIP launch (the reference's tensor ops + write)
+            p = f"l{i}."
             q = paged.write_rope(i, qkv, self.w[p + "qn"], self.w[p + "kn"], self.cos, self.sin, c.eps)
-            y = paged.attend(i, q)  # (B, H, 1, D)
-            x = x + F.linear(y.transpose(1, 2).reshape(x.shape[0], 1, -1), self.w[f"l{i}.wo"])
-            x = x + self._mlp(i, rms_norm(x, self.w[f"l{i}.ln2"], c.eps))
+            return paged.attend(i, q).reshape(B, -1)
+
+        h = self._decode_stack(x, attend)
         paged.advance()
-        return self.logits(x[:, 0])
+        return F.linear(h, self.w["embed"])
 
 
 class GraphDecoder:
@@ -224,17 +275,15 @@ class GraphDecoder:
         m, c, bs = self.model, self.model.cfg, self.pool.block_size
         self.seqlen.copy_((self.pos + 1).to(torch.int32))
         slots = self.table64.gather(1, (self.pos // bs).view(-1, 1)).view(-1) * bs + self.pos % bs
-        x = F.embedding(self.tokens.view(-1, 1), m.w["embed"])
-        for i in range(c.n_layer):
+        x = F.embedding(self.tokens, m.w["embed"])  # (B, C)
+
+        def attend(i: int, qkv: torch.Tensor) -> torch.Tensor:
             p = f"l{i}."
-            h = rms_norm(x, m.w[p + "ln1"], c.eps)
-            qkv = F.linear(h, m.w[p + "wqkv"]).view(self.B, -1)
             q = self.pool.write_qk_norm_rope(i, slots, qkv, m.w[p + "qn"], m.w[p + "kn"], m.cos, m.sin,
                                              self.pos, c.eps)
-            y = self.plan.run(i, q)  # (B, H, D)
-            x = x + F.linear(y.reshape(self.B, 1, -1), m.w[f"l{i}.wo"])
-            x = x + m._mlp(i, rms_norm(x, m.w[f"l{i}.ln2"], c.eps))
-        nxt = m.logits(x[:, 0]).argmax(-1)
+            return self.plan.run(i, q).view(self.B, -1)
+
+        nxt = F.linear(m._decode_stack(x, attend), m.w["embed"]).argmax(-1)
         self.history.index_copy_(1, self.step_idx, nxt.view(-1, 1))
         self.tokens.copy_(nxt)
         self.pos.add_(1)

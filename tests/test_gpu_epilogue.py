@@ -99,3 +99,48 @@ def test_epilogue_validates_shapes():
         pool.write_qk_norm_rope(0, slots, qkv, qn, kn, cos, sin, pos.int(), 1e-6)
     with pytest.raises(ValueError, match="cos/sin"):
         pool.write_qk_norm_rope(0, slots, qkv, qn, kn, cos[:, 1:], sin[:, 1:], pos, 1e-6)
+
+
+# ---------------------------------------------------------------- decode-step small ops
+from miattn.qwen3 import add_rms_norm, silu_mul  # noqa: E402
+import torch.nn.functional as F  # noqa: E402
+
+
+@pytest.mark.parametrize("rows,cols", [(32, 1024), (3, 4096), (5, 200)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("with_delta", [True, False])
+def test_add_rms_norm_matches_the_reference_op_chain(rows, cols, dtype, with_delta):
+    g = torch.Generator().manual_seed(rows * cols)
+    x = torch.randn(rows, cols, generator=g).to(dtype).cuda()
+    d = torch.randn(rows, cols, generator=g).to(dtype).cuda() if with_delta else None
+    w = (1.0 + 0.1 * torch.randn(cols, generator=g)).to(dtype).cuda()
+    s_ref = x + d if with_delta else x.clone()
+    h_ref = rms_norm(s_ref, w, 1e-6)
+    xs = x.clone()
+    x_out, h = add_rms_norm(xs, d, w, 1e-6)
+    torch.cuda.synchronize()
+    assert x_out is xs and torch.equal(xs, s_ref)  # the residual add is exact per element
+    same = (h == h_ref).float().mean().item()
+    assert same > 0.999, f"only {same:.4%} equal"
+    assert _ulps(h, h_ref, dtype) <= 2.0
+
+
+@pytest.mark.parametrize("rows,inter", [(32, 3072), (7, 100)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_silu_mul_matches_the_reference_op_chain(rows, inter, dtype):
+    g = torch.Generator().manual_seed(rows + inter)
+    gu = (torch.randn(rows, 2 * inter, generator=g) * 3).to(dtype).cuda()
+    want = F.silu(gu[:, :inter]) * gu[:, inter:]
+    got = silu_mul(gu)
+    torch.cuda.synchronize()
+    same = (got == want).float().mean().item()
+    assert same > 0.999, f"only {same:.4%} equal"
+    assert _ulps(got, want, dtype) <= 2.0
+
+
+def test_decode_step_ops_reject_bad_shapes():
+    x = torch.zeros(4, 8, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError, match="delta"):
+        add_rms_norm(x, x[:, :4].contiguous(), torch.ones(8, dtype=torch.bfloat16, device="cuda"), 1e-6)
+    with pytest.raises(ValueError, match="gate_up"):
+        silu_mul(torch.zeros(4, 7, dtype=torch.bfloat16, device="cuda"))
