@@ -218,7 +218,8 @@ def bench_tpot(stream, prompt_len: int = 1920, new_tokens: int = 128, B: int = 3
     """Config 5 shape, closed batch: random-init Qwen3-0.6B, B rows of ``prompt_len`` random
     tokens prefilled in one packed group, then ``new_tokens`` greedy decode steps (context
     ``prompt_len`` -> ``prompt_len + new_tokens``). TPOT = GPU time of one whole decode step
-    (28 layers: projections, norms, RoPE, HIP slot write, HIP paged decode, MLP, lm_head,
+    (28 layers: projections, the HIP q/k-norm + RoPE + K/V write epilogue, HIP paged decode,
+    HIP residual add + RMSNorm and SiLU * up, the MLP GEMMs, lm_head,
     argmax), replayed from one HIP graph; the eager (Python-launched) step is reported too."""
     from miattn import PagedKV
     from miattn.qwen3 import GraphDecoder, Qwen3, Qwen3Config, random_weights
