@@ -17,6 +17,9 @@
  *   mi_add_rms_norm,   decode-step small ops   residual add + RMSNorm, SiLU(gate) * up
  *   mi_silu_mul                                (reference model/layers.py:365-367, :342-350,
  *                                              :325-335)
+ *   mi_rows_gemm       decode-step projections nn.Linear at a few rows: q/k/v, o, gate/up,
+ *                                              down, lm_head (reference model/layers.py:176-222,
+ *                                              :325-335; model/minillm.py lm_head)
  *
  * Conventions shared by every entry point:
  *   - every pointer except the `host_*` arguments is a device pointer;
@@ -88,8 +91,10 @@ int mi_kv_slot_write(const void* k, const void* v, const void* slot_ids, int slo
  * activation dtype (see csrc/decode_epilogue.hip). slot_ids as for mi_kv_slot_write (int32 or
  * int64 per slot_bits; pools (n_slots, H_kv, D) contiguous). A row whose position is outside
  * [0, n_pos) or whose slot is outside [0, n_slots) is not written and 1 + its index goes to
- * *error_word (may be NULL). D = 64, 128 or 256. */
-int mi_qk_norm_rope_write(const void* qkv, int64_t row_stride, const void* q_norm_w,
+ * *error_word (may be NULL). D = 64, 128 or 256. qkv_parts = 0: qkv holds `dtype` values;
+ * qkv_parts = n >= 1: qkv holds fp32 split-K partial sums [n][B][row_stride] (mi_rows_gemm
+ * with n_split = n), summed in split order and rounded once to `dtype` before the above. */
+int mi_qk_norm_rope_write(const void* qkv, int64_t row_stride, int qkv_parts, const void* q_norm_w,
                           const void* k_norm_w, const void* cos_tab, const void* sin_tab,
                           int64_t n_pos, const int64_t* pos, const void* slot_ids, int slot_bits,
                           void* q_out, void* k_pool, void* v_pool, int B, int H, int H_kv, int D,
@@ -104,10 +109,28 @@ int mi_qk_norm_rope_write(const void* qkv, int64_t row_stride, const void* q_nor
  *   x_out = s (may be NULL, may alias x); h_out = s / sqrt(mean(s^2) + eps) * weight.
  *   cols <= 4096.
  * mi_silu_mul: gate_up (rows, 2 * inter) contiguous rows [gate | up];
- *   out (rows, inter) = silu(gate) * up. */
-int mi_add_rms_norm(const void* x, const void* delta, const void* weight, void* x_out, void* h_out,
-                    int rows, int cols, float eps, int dtype, void* stream);
-int mi_silu_mul(const void* gate_up, void* out, int rows, int inter, int dtype, void* stream);
+ *   out (rows, inter) = silu(gate) * up.
+ * delta_parts / gate_up_parts = 0: that input holds `dtype` values; n >= 1: it holds fp32
+ * split-K partial sums [n][rows][cols] of mi_rows_gemm, summed in split order and rounded
+ * once to `dtype` (the projection output's own rounding) before the chain above. */
+int mi_add_rms_norm(const void* x, const void* delta, int delta_parts, const void* weight, void* x_out,
+                    void* h_out, int rows, int cols, float eps, int dtype, void* stream);
+int mi_silu_mul(const void* gate_up, int gate_up_parts, void* out, int rows, int inter, int dtype,
+                void* stream);
+
+/* ------------------------------------------------------------------ decode-step projections
+ * out = a w^T for 1 <= M <= 32 rows (nn.Linear without bias, the reference's projections at
+ * decode batch = running sequences). a (M, K), w (N, K), both with unit element stride, row
+ * strides lda / ldw (multiples of 8, 16-byte aligned rows); bf16 or fp16.
+ * n_split = 1: out (M, N) row stride ldo, in `dtype` (fp32 accumulation, rounded once).
+ * n_split = S > 1: K is split S ways; partials (S, M, N) fp32 contiguous receive each
+ *   split's sums, for a consumer that sums them (the *_parts arguments above). Needs
+ *   K % (S * 256) == 0 and K / S <= 1024. One launch of ceil(N / 32) x S workgroups.
+ * mi_rows_gemm_split returns the split the launcher is tuned for at that shape (0 if K is
+ * not a multiple of 256). */
+int mi_rows_gemm_split(int M, int N, int K);
+int mi_rows_gemm(const void* a, int64_t lda, const void* w, int64_t ldw, void* out, int64_t ldo,
+                 float* partials, int M, int N, int K, int n_split, int dtype, void* stream);
 
 /* ------------------------------------------------------------------ paged decode
  * Replaces paged_decode (reference model/triton_decode.py:250-328) and its kernel

@@ -72,6 +72,18 @@ __device__ __forceinline__ void store16(void* p, const uint4& v) {
   *reinterpret_cast<uint4*>(p) = v;
 }
 
+// 16-byte global load and store with the nontemporal (streaming) hint, for data that one
+// kernel touches once.
+typedef unsigned u32x4_nt __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 load16_nt(const void* p) {
+  const u32x4_nt w = __builtin_nontemporal_load(reinterpret_cast<const u32x4_nt*>(p));
+  return make_uint4(w.x, w.y, w.z, w.w);
+}
+__device__ __forceinline__ void store16_nt(void* p, const uint4& v) {
+  const u32x4_nt w = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(w, reinterpret_cast<u32x4_nt*>(p));
+}
+
 // ------------------------------------------------------------------ cross-lane reductions
 // DPP butterflies inside one 16-lane DPP row. quad_perm [1,0,3,2] and [2,3,0,1] exchange
 // lanes xor 1 and xor 2; once every quad holds one value, row_half_mirror (lane i <- 7-i)

@@ -18,7 +18,9 @@
 //
 // Layout: one wave per (row, head) over q, k and v heads of a packed projection row
 // [q (H x D) | k (H_kv x D) | v (H_kv x D)]; lane l holds the rotation pairs (p, p + D/2)
-// for p = l, l + 64, ... < D/2, so the pair partner is in the same lane.
+// for p = l, l + 64, ... < D/2, so the pair partner is in the same lane. The projection
+// rows are T, or fp32 split-K partial sums [parts][B][row_stride] of mi_rows_gemm, summed
+// in split order and rounded once to T (the value the projection's own output would hold).
 #include "common.h"
 
 namespace miattn {
@@ -36,7 +38,8 @@ __device__ __forceinline__ float rt(float x) {
 
 template <typename T, int D, typename IdxT>
 __global__ __launch_bounds__(256) void qk_norm_rope_write_kernel(
-    const T* __restrict__ qkv, int64_t row_stride, const T* __restrict__ q_w, const T* __restrict__ k_w,
+    const void* __restrict__ qkv, int64_t row_stride, int parts, int64_t plane, const T* __restrict__ q_w,
+    const T* __restrict__ k_w,
     const T* __restrict__ cos_tab, const T* __restrict__ sin_tab, int64_t n_pos,
     const int64_t* __restrict__ pos, const IdxT* __restrict__ slots, T* __restrict__ q_out,
     T* __restrict__ k_pool, T* __restrict__ v_pool, int B, int H, int H_kv, int64_t n_slots,
@@ -56,24 +59,31 @@ __global__ __launch_bounds__(256) void qk_norm_rope_write_kernel(
     if (lane == 0 && head == 0 && err != nullptr) atomicCAS(err, 0, b + 1);
     return;
   }
-  const T* src = qkv + int64_t(b) * row_stride + int64_t(head) * D;
+  const int64_t src = int64_t(b) * row_stride + int64_t(head) * D;
+  auto in = [&](int p) {
+    if (parts == 0) return to_f32(static_cast<const T*>(qkv)[src + p]);
+    const float* f = static_cast<const float*>(qkv) + src + p;
+    float acc = f[0];
+    for (int sp = 1; sp < parts; ++sp) acc += f[sp * plane];
+    return rt<T>(acc);
+  };
 
   float x1[PPL], x2[PPL];
 #pragma unroll
   for (int j = 0; j < PPL; ++j) {
     const int p = lane + 64 * j;
-    x1[j] = p < HALF ? to_f32(src[p]) : 0.0f;
-    x2[j] = p < HALF ? to_f32(src[p + HALF]) : 0.0f;
+    x1[j] = p < HALF ? in(p) : 0.0f;
+    x2[j] = p < HALF ? in(p + HALF) : 0.0f;
   }
 
-  if (head >= H + H_kv) {  // v head: copied as is
+  if (head >= H + H_kv) {  // v head: copied as is (exact: x1/x2 hold T values)
     T* dst = v_pool + (int64_t(slot) * H_kv + (head - H - H_kv)) * D;
 #pragma unroll
     for (int j = 0; j < PPL; ++j) {
       const int p = lane + 64 * j;
       if (p < HALF) {
-        dst[p] = src[p];
-        dst[p + HALF] = src[p + HALF];
+        dst[p] = from_f32<T>(x1[j]);
+        dst[p + HALF] = from_f32<T>(x2[j]);
       }
     }
     return;
@@ -121,17 +131,17 @@ __global__ __launch_bounds__(256) void qk_norm_rope_write_kernel(
 }
 
 template <typename T, int D>
-int launch_d(const void* qkv, int64_t row_stride, const void* q_w, const void* k_w, const void* cos_tab,
+int launch_d(const void* qkv, int64_t row_stride, int parts, const void* q_w, const void* k_w, const void* cos_tab,
              const void* sin_tab, int64_t n_pos, const int64_t* pos, const void* slots, int slot_bits,
              void* q_out, void* k_pool, void* v_pool, int B, int H, int H_kv, int64_t n_slots, float eps,
              int32_t* err, hipStream_t s) {
   constexpr int kWaves = 4;
   const dim3 grid((H + 2 * H_kv + kWaves - 1) / kWaves, B);
-  const T* qkv_t = static_cast<const T*>(qkv);
+  const int64_t plane = int64_t(B) * row_stride;
   auto go = [&](auto idx_tag) {
     using IdxT = decltype(idx_tag);
-    hipLaunchKernelGGL((qk_norm_rope_write_kernel<T, D, IdxT>), grid, dim3(64 * kWaves), 0, s, qkv_t,
-                       row_stride, static_cast<const T*>(q_w), static_cast<const T*>(k_w),
+    hipLaunchKernelGGL((qk_norm_rope_write_kernel<T, D, IdxT>), grid, dim3(64 * kWaves), 0, s, qkv,
+                       row_stride, parts, plane, static_cast<const T*>(q_w), static_cast<const T*>(k_w),
                        static_cast<const T*>(cos_tab), static_cast<const T*>(sin_tab), n_pos, pos,
                        static_cast<const IdxT*>(slots), static_cast<T*>(q_out), static_cast<T*>(k_pool),
                        static_cast<T*>(v_pool), B, H, H_kv, n_slots, eps, err);
@@ -141,16 +151,16 @@ int launch_d(const void* qkv, int64_t row_stride, const void* q_w, const void* k
 }
 
 template <typename T>
-int launch_t(int D, const void* qkv, int64_t row_stride, const void* q_w, const void* k_w, const void* cos_tab,
+int launch_t(int D, const void* qkv, int64_t row_stride, int parts, const void* q_w, const void* k_w, const void* cos_tab,
              const void* sin_tab, int64_t n_pos, const int64_t* pos, const void* slots, int slot_bits,
              void* q_out, void* k_pool, void* v_pool, int B, int H, int H_kv, int64_t n_slots, float eps,
              int32_t* err, hipStream_t s) {
   switch (D) {
-    case 64: return launch_d<T, 64>(qkv, row_stride, q_w, k_w, cos_tab, sin_tab, n_pos, pos, slots, slot_bits,
+    case 64: return launch_d<T, 64>(qkv, row_stride, parts, q_w, k_w, cos_tab, sin_tab, n_pos, pos, slots, slot_bits,
                                     q_out, k_pool, v_pool, B, H, H_kv, n_slots, eps, err, s);
-    case 128: return launch_d<T, 128>(qkv, row_stride, q_w, k_w, cos_tab, sin_tab, n_pos, pos, slots, slot_bits,
+    case 128: return launch_d<T, 128>(qkv, row_stride, parts, q_w, k_w, cos_tab, sin_tab, n_pos, pos, slots, slot_bits,
                                       q_out, k_pool, v_pool, B, H, H_kv, n_slots, eps, err, s);
-    case 256: return launch_d<T, 256>(qkv, row_stride, q_w, k_w, cos_tab, sin_tab, n_pos, pos, slots, slot_bits,
+    case 256: return launch_d<T, 256>(qkv, row_stride, parts, q_w, k_w, cos_tab, sin_tab, n_pos, pos, slots, slot_bits,
                                       q_out, k_pool, v_pool, B, H, H_kv, n_slots, eps, err, s);
     default:
       return fail(MI_ERR_UNSUPPORTED, "mi_qk_norm_rope_write: head_dim %d is not supported (64, 128, 256)", D);
@@ -160,7 +170,7 @@ int launch_t(int D, const void* qkv, int64_t row_stride, const void* q_w, const 
 }  // namespace
 }  // namespace miattn
 
-extern "C" int mi_qk_norm_rope_write(const void* qkv, int64_t row_stride, const void* q_norm_w,
+extern "C" int mi_qk_norm_rope_write(const void* qkv, int64_t row_stride, int qkv_parts, const void* q_norm_w,
                                      const void* k_norm_w, const void* cos_tab, const void* sin_tab,
                                      int64_t n_pos, const int64_t* pos, const void* slot_ids, int slot_bits,
                                      void* q_out, void* k_pool, void* v_pool, int B, int H, int H_kv, int D,
@@ -173,6 +183,7 @@ extern "C" int mi_qk_norm_rope_write(const void* qkv, int64_t row_stride, const 
     return fail(MI_ERR_INVALID, "mi_qk_norm_rope_write: slot_bits must be 32 or 64, got %d", slot_bits);
   }
   if (n_pos < 1) return fail(MI_ERR_INVALID, "mi_qk_norm_rope_write: the RoPE table is empty");
+  if (qkv_parts < 0) return fail(MI_ERR_INVALID, "mi_qk_norm_rope_write: qkv_parts %d < 0", qkv_parts);
   if (row_stride < int64_t(H + 2 * H_kv) * D) {
     return fail(MI_ERR_INVALID, "mi_qk_norm_rope_write: row stride %lld < %d packed q/k/v elements",
                 (long long)row_stride, (H + 2 * H_kv) * D);
@@ -185,13 +196,13 @@ extern "C" int mi_qk_norm_rope_write(const void* qkv, int64_t row_stride, const 
   if (B > 65535) return fail(MI_ERR_UNSUPPORTED, "mi_qk_norm_rope_write: at most 65535 rows, got %d", B);
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
-    case MI_BF16: return launch_t<bf16_t>(D, qkv, row_stride, q_norm_w, k_norm_w, cos_tab, sin_tab, n_pos, pos,
+    case MI_BF16: return launch_t<bf16_t>(D, qkv, row_stride, qkv_parts, q_norm_w, k_norm_w, cos_tab, sin_tab, n_pos, pos,
                                           slot_ids, slot_bits, q_out, k_pool, v_pool, B, H, H_kv, n_slots, eps,
                                           error_word, s);
-    case MI_F16: return launch_t<f16_t>(D, qkv, row_stride, q_norm_w, k_norm_w, cos_tab, sin_tab, n_pos, pos,
+    case MI_F16: return launch_t<f16_t>(D, qkv, row_stride, qkv_parts, q_norm_w, k_norm_w, cos_tab, sin_tab, n_pos, pos,
                                         slot_ids, slot_bits, q_out, k_pool, v_pool, B, H, H_kv, n_slots, eps,
                                         error_word, s);
-    case MI_F32: return launch_t<float>(D, qkv, row_stride, q_norm_w, k_norm_w, cos_tab, sin_tab, n_pos, pos,
+    case MI_F32: return launch_t<float>(D, qkv, row_stride, qkv_parts, q_norm_w, k_norm_w, cos_tab, sin_tab, n_pos, pos,
                                         slot_ids, slot_bits, q_out, k_pool, v_pool, B, H, H_kv, n_slots, eps,
                                         error_word, s);
     default:

@@ -13,6 +13,11 @@
 // rounded, times w rounded; silu(g) = g / (1 + exp(-g)) in fp32 rounded, times u rounded.
 // Results equal the tensor-op chain's except where the fp32 sum's order moves a rounding
 // boundary of the mean.
+//
+// The projection feeding each op (o_proj / down_proj into the add, gate_up into SiLU * up)
+// may arrive as fp32 split-K partial sums [parts][rows][cols] of mi_rows_gemm: the op sums
+// them in split order and rounds once to the activation dtype, the value the projection's
+// own output would hold, before the chain above.
 #include "common.h"
 
 namespace miattn {
@@ -26,13 +31,28 @@ __device__ __forceinline__ float rnd(float x) {
   return to_f32(from_f32<T>(x));
 }
 
+// Element (row, col) of a projection output: T, or the rounded sum of fp32 partials.
+template <typename T>
+struct ProjIn {
+  const void* p;
+  int parts;      // 0: p is T [rows][cols]; n >= 1: p is fp32 [n][rows][cols]
+  int64_t plane;  // rows * cols
+  __device__ __forceinline__ float at(int64_t idx) const {
+    if (parts == 0) return to_f32(static_cast<const T*>(p)[idx]);
+    const float* f = static_cast<const float*>(p);
+    float acc = f[idx];
+    for (int s = 1; s < parts; ++s) acc += f[s * plane + idx];
+    return rnd<T>(acc);
+  }
+};
+
 constexpr int kNormThreads = 256;
 constexpr int kNormMaxPerThread = 16;  // rows of up to 4096 elements stay in registers
 
 // One workgroup per row: s = x + delta (or x), x_out = s, h_out = rmsnorm(s) * w.
 template <typename T, bool kAdd>
 __global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(
-    const T* x, const T* __restrict__ delta, const T* __restrict__ w, T* x_out,  // x_out may alias x
+    const T* x, ProjIn<T> delta, const T* __restrict__ w, T* x_out,  // x_out may alias x
     T* __restrict__ h_out, int cols, float eps) {
   __shared__ float part[kNormThreads / 64];
   const int64_t row = blockIdx.x;
@@ -46,7 +66,7 @@ __global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(
     s[j] = 0.0f;
     if (i < cols) {
       float v = to_f32(xr[i]);
-      if constexpr (kAdd) v = rnd<T>(v + to_f32(delta[row * cols + i]));
+      if constexpr (kAdd) v = rnd<T>(v + delta.at(row * cols + i));
       s[j] = v;
       ss += rnd<T>(v * v);
     }
@@ -73,47 +93,47 @@ __global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(
 
 // out[r, i] = silu(gu[r, i]) * gu[r, inter + i]
 template <typename T>
-__global__ __launch_bounds__(256) void silu_mul_kernel(const T* __restrict__ gu, T* __restrict__ out, int inter) {
+__global__ __launch_bounds__(256) void silu_mul_kernel(ProjIn<T> gu, T* __restrict__ out, int inter) {
   const int64_t row = blockIdx.y;
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= inter) return;
-  const float g = to_f32(gu[row * 2 * inter + i]);
-  const float u = to_f32(gu[row * 2 * inter + inter + i]);
+  const float g = gu.at(row * 2 * inter + i);
+  const float u = gu.at(row * 2 * inter + inter + i);
   const float sg = rnd<T>(g / (1.0f + expf(-g)));
   out[row * inter + i] = from_f32<T>(rnd<T>(sg * u));
 }
 
 template <typename T>
-int launch_norm(const void* x, const void* delta, const void* w, void* x_out, void* h_out, int rows, int cols,
-                float eps, hipStream_t s) {
+int launch_norm(const void* x, const void* delta, int delta_parts, const void* w, void* x_out, void* h_out,
+                int rows, int cols, float eps, hipStream_t s) {
   const dim3 grid(rows), block(kNormThreads);
+  const ProjIn<T> d{delta, delta_parts, int64_t(rows) * cols};
   if (delta != nullptr) {
-    hipLaunchKernelGGL((add_rms_norm_kernel<T, true>), grid, block, 0, s, static_cast<const T*>(x),
-                       static_cast<const T*>(delta), static_cast<const T*>(w), static_cast<T*>(x_out),
-                       static_cast<T*>(h_out), cols, eps);
+    hipLaunchKernelGGL((add_rms_norm_kernel<T, true>), grid, block, 0, s, static_cast<const T*>(x), d,
+                       static_cast<const T*>(w), static_cast<T*>(x_out), static_cast<T*>(h_out), cols, eps);
   } else {
-    hipLaunchKernelGGL((add_rms_norm_kernel<T, false>), grid, block, 0, s, static_cast<const T*>(x),
-                       static_cast<const T*>(nullptr), static_cast<const T*>(w), static_cast<T*>(nullptr),
-                       static_cast<T*>(h_out), cols, eps);
+    hipLaunchKernelGGL((add_rms_norm_kernel<T, false>), grid, block, 0, s, static_cast<const T*>(x), d,
+                       static_cast<const T*>(w), static_cast<T*>(nullptr), static_cast<T*>(h_out), cols, eps);
   }
   return launch_status("mi_add_rms_norm");
 }
 
 template <typename T>
-int launch_silu(const void* gu, void* out, int rows, int inter, hipStream_t s) {
+int launch_silu(const void* gu, int gu_parts, void* out, int rows, int inter, hipStream_t s) {
   const dim3 grid((inter + 255) / 256, rows);
-  hipLaunchKernelGGL((silu_mul_kernel<T>), grid, dim3(256), 0, s, static_cast<const T*>(gu), static_cast<T*>(out),
-                     inter);
+  const ProjIn<T> g{gu, gu_parts, int64_t(rows) * 2 * inter};
+  hipLaunchKernelGGL((silu_mul_kernel<T>), grid, dim3(256), 0, s, g, static_cast<T*>(out), inter);
   return launch_status("mi_silu_mul");
 }
 
 }  // namespace
 }  // namespace miattn
 
-extern "C" int mi_add_rms_norm(const void* x, const void* delta, const void* weight, void* x_out, void* h_out,
-                               int rows, int cols, float eps, int dtype, void* stream) {
+extern "C" int mi_add_rms_norm(const void* x, const void* delta, int delta_parts, const void* weight, void* x_out,
+                               void* h_out, int rows, int cols, float eps, int dtype, void* stream) {
   using namespace miattn;
   if (rows < 0 || cols < 1) return fail(MI_ERR_INVALID, "mi_add_rms_norm: bad shape (%d, %d)", rows, cols);
+  if (delta_parts < 0) return fail(MI_ERR_INVALID, "mi_add_rms_norm: delta_parts %d < 0", delta_parts);
   if (cols > kNormThreads * kNormMaxPerThread) {
     return fail(MI_ERR_UNSUPPORTED, "mi_add_rms_norm: rows of at most %d elements, got %d",
                 kNormThreads * kNormMaxPerThread, cols);
@@ -123,25 +143,27 @@ extern "C" int mi_add_rms_norm(const void* x, const void* delta, const void* wei
   if (rows > 2147483647 / cols) return fail(MI_ERR_UNSUPPORTED, "mi_add_rms_norm: too many elements");
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
-    case MI_BF16: return launch_norm<bf16_t>(x, delta, weight, x_out, h_out, rows, cols, eps, s);
-    case MI_F16: return launch_norm<f16_t>(x, delta, weight, x_out, h_out, rows, cols, eps, s);
-    case MI_F32: return launch_norm<float>(x, delta, weight, x_out, h_out, rows, cols, eps, s);
+    case MI_BF16: return launch_norm<bf16_t>(x, delta, delta_parts, weight, x_out, h_out, rows, cols, eps, s);
+    case MI_F16: return launch_norm<f16_t>(x, delta, delta_parts, weight, x_out, h_out, rows, cols, eps, s);
+    case MI_F32: return launch_norm<float>(x, delta, delta_parts, weight, x_out, h_out, rows, cols, eps, s);
     default: return fail(MI_ERR_INVALID, "mi_add_rms_norm: unknown dtype %d", dtype);
   }
 }
 
-extern "C" int mi_silu_mul(const void* gate_up, void* out, int rows, int inter, int dtype, void* stream) {
+extern "C" int mi_silu_mul(const void* gate_up, int gate_up_parts, void* out, int rows, int inter, int dtype,
+                           void* stream) {
   using namespace miattn;
   if (rows < 0 || inter < 1) return fail(MI_ERR_INVALID, "mi_silu_mul: bad shape (%d, %d)", rows, inter);
+  if (gate_up_parts < 0) return fail(MI_ERR_INVALID, "mi_silu_mul: gate_up_parts %d < 0", gate_up_parts);
   if (gate_up == nullptr || out == nullptr) return fail(MI_ERR_INVALID, "mi_silu_mul: NULL pointer");
   if (rows == 0) return MI_OK;
   if (rows > 65535) return fail(MI_ERR_UNSUPPORTED, "mi_silu_mul: at most 65535 rows, got %d", rows);
   if (int64_t(rows) * 2 * inter > 2147483647LL) return fail(MI_ERR_UNSUPPORTED, "mi_silu_mul: too many elements");
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
-    case MI_BF16: return launch_silu<bf16_t>(gate_up, out, rows, inter, s);
-    case MI_F16: return launch_silu<f16_t>(gate_up, out, rows, inter, s);
-    case MI_F32: return launch_silu<float>(gate_up, out, rows, inter, s);
+    case MI_BF16: return launch_silu<bf16_t>(gate_up, gate_up_parts, out, rows, inter, s);
+    case MI_F16: return launch_silu<f16_t>(gate_up, gate_up_parts, out, rows, inter, s);
+    case MI_F32: return launch_silu<float>(gate_up, gate_up_parts, out, rows, inter, s);
     default: return fail(MI_ERR_INVALID, "mi_silu_mul: unknown dtype %d", dtype);
   }
 }

@@ -1366,13 +1366,6 @@ struct Duo {
   }
 };
 
-// 16-byte global store with the nontemporal (streaming) hint.
-__device__ __forceinline__ void store16_nt(void* p, const uint4& v) {
-  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-  const u32x4 w = {v.x, v.y, v.z, v.w};
-  __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(p));
-}
-
 // s_waitcnt lgkmcnt(0) alone (vmcnt and expcnt left at their maximum).
 __device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14)); }
 

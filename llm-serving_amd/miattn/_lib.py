@@ -73,12 +73,19 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "mi_varlen_workspace_size": (_c_size_t, [_p_int32, _c_int]),
     "mi_add_rms_norm": (
-        _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_float, _c_int, _c_void_p]
+        _c_int,
+        [_c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_float, _c_int, _c_void_p],
     ),
-    "mi_silu_mul": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_void_p]),
+    "mi_silu_mul": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_int, _c_int, _c_int, _c_void_p]),
+    "mi_rows_gemm_split": (_c_int, [_c_int, _c_int, _c_int]),
+    "mi_rows_gemm": (
+        _c_int,
+        [_c_void_p, _c_int64, _c_void_p, _c_int64, _c_void_p, _c_int64, _c_void_p, _c_int, _c_int, _c_int,
+         _c_int, _c_int, _c_void_p],
+    ),
     "mi_qk_norm_rope_write": (
         _c_int,
-        [_c_void_p, _c_int64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int64, _c_void_p,
+        [_c_void_p, _c_int64, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int64, _c_void_p,
          _c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int,
          _c_int64, _c_float, _c_int, _c_void_p, _c_void_p],
     ),
@@ -90,7 +97,7 @@ SIGNATURES: dict[str, tuple] = {
     ),
 }
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 
 def _load():

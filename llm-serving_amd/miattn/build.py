@@ -37,7 +37,7 @@ HIPCC_FLAGS = [
 ]
 
 SOURCES = ["capi.hip", "slot_write.hip", "paged_decode.hip", "varlen_prefill.hip", "decode_epilogue.hip",
-           "decode_step.hip"]
+           "decode_step.hip", "rows_gemm.hip"]
 
 
 def _hipcc() -> str:

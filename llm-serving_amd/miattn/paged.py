@@ -25,6 +25,7 @@ import torch
 
 from . import _lib
 from .decode import TRITON_AVAILABLE, paged_decode_plan
+from .rows import Parts
 
 __all__ = ["PagedPool", "PagedKV", "PagedWriteSink"]
 
@@ -172,7 +173,7 @@ class PagedPool:
         if self.strict_writes:
             self.check_writes()
 
-    def write_qk_norm_rope(self, layer: int, slot_ids: torch.Tensor, qkv: torch.Tensor,
+    def write_qk_norm_rope(self, layer: int, slot_ids: torch.Tensor, qkv,
                            q_norm_w: torch.Tensor, k_norm_w: torch.Tensor, cos: torch.Tensor,
                            sin: torch.Tensor, pos: torch.Tensor, eps: float) -> torch.Tensor:
         """One decode step's attention epilogue in one HIP launch: per-head RMSNorm of q and k
@@ -181,7 +182,8 @@ class PagedPool:
         at ``slot_ids``; returns q ``(B, n_head, head_dim)``, contiguous for the paged decode.
 
         ``qkv`` is the packed projection output ``(B, (n_head + 2 * n_kv_head) * head_dim)``
-        (rows ``[q | k | v]``, unit element stride). The reference runs this as tensor ops
+        (rows ``[q | k | v]``, unit element stride), or its split-K partial sums
+        (:class:`~miattn.rows.Parts`, summed and rounded once). The reference runs this as tensor ops
         (``model/layers.py:193-211``: q_norm/k_norm, ``apply_rotary_emb``) followed by
         ``PagedKV.write`` (``model/paged.py:503-520``); the kernel rounds each step to the
         pool dtype as those ops do. A row whose position is outside the tables or whose slot
@@ -189,11 +191,17 @@ class PagedPool:
         """
         layer = self._check_layer(layer)
         H, H_kv, D = self.n_head, self.n_kv_head, self.head_dim
-        if qkv.dim() != 2 or qkv.shape[1] != (H + 2 * H_kv) * D or qkv.stride(1) != 1:
-            raise ValueError(
-                f"qkv must be (B, {(H + 2 * H_kv) * D}) with unit element stride, got {tuple(qkv.shape)} "
-                f"strides {tuple(qkv.stride())}"
-            )
+        if isinstance(qkv, Parts):
+            if qkv.shape[1] != (H + 2 * H_kv) * D:
+                raise ValueError(f"qkv must be (B, {(H + 2 * H_kv) * D}), got partial sums of {qkv.shape}")
+            qkv_ptr, qkv_row, qkv_parts, qkv_data = qkv.data.data_ptr(), qkv.shape[1], qkv.n_parts, qkv.data
+        else:
+            if qkv.dim() != 2 or qkv.shape[1] != (H + 2 * H_kv) * D or qkv.stride(1) != 1:
+                raise ValueError(
+                    f"qkv must be (B, {(H + 2 * H_kv) * D}) with unit element stride, got {tuple(qkv.shape)} "
+                    f"strides {tuple(qkv.stride())}"
+                )
+            qkv_ptr, qkv_row, qkv_parts, qkv_data = qkv.data_ptr(), qkv.stride(0), 0, qkv
         B = int(qkv.shape[0])
         for name, t, shape in (("q_norm_w", q_norm_w, (D,)), ("k_norm_w", k_norm_w, (D,))):
             if tuple(t.shape) != shape or not t.is_contiguous():
@@ -210,14 +218,14 @@ class PagedPool:
             if t.dtype != self.dtype:
                 raise ValueError(f"{name} is {t.dtype}, the pool holds {self.dtype}")
         _lib.require_library("PagedPool.write_qk_norm_rope")
-        tensors = (qkv, q_norm_w, k_norm_w, cos, sin, pos, slot_ids)
+        tensors = (qkv_data, q_norm_w, k_norm_w, cos, sin, pos, slot_ids)
         if self.device.type != "cuda" or not all(t.is_cuda for t in tensors):
             raise RuntimeError("PagedPool.write_qk_norm_rope is a HIP kernel and needs CUDA (HIP) tensors")
         slot_ids = slot_ids.contiguous()
         pos = pos.contiguous()
         q = torch.empty((B, H, D), dtype=self.dtype, device=self.device)
         rc = _lib.lib.mi_qk_norm_rope_write(
-            qkv.data_ptr(), qkv.stride(0), q_norm_w.data_ptr(), k_norm_w.data_ptr(), cos.data_ptr(),
+            qkv_ptr, qkv_row, qkv_parts, q_norm_w.data_ptr(), k_norm_w.data_ptr(), cos.data_ptr(),
             sin.data_ptr(), cos.shape[0], pos.data_ptr(), slot_ids.data_ptr(),
             32 if slot_ids.dtype == torch.int32 else 64, q.data_ptr(), self.keys[layer].data_ptr(),
             self.values[layer].data_ptr(), B, H, H_kv, D, self.n_slots, float(eps),

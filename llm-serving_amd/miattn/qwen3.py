@@ -8,11 +8,12 @@ goes through :class:`~miattn.packed.PackedPrefill` (HIP varlen kernel + one slot
 launch per layer) and decode through :class:`~miattn.paged.PagedKV` (HIP slot write +
 block-table decode), exactly the containers the reference's layers call
 (reference ``model/layers.py:217-250``). Projections and the residual-stream norms are
-plain torch; in decode, the q/k norms, RoPE and the K/V write run as one HIP launch per
-layer (``PagedPool.write_qk_norm_rope``) over one projection GEMM of the stacked q/k/v
-weights, each residual add with the next RMSNorm is one launch (``add_rms_norm``) and the
-MLP's SiLU * up another (``silu_mul``), all with the reference ops' rounding (prefill keeps
-the tensor ops).
+plain torch in prefill. In decode every projection and the lm_head is one HIP rows-GEMM
+launch (``rows_linear``, q/k/v and gate/up over stacked weights), the q/k norms, RoPE and the
+K/V write are one HIP launch per layer (``PagedPool.write_qk_norm_rope``), each residual add
+with the next RMSNorm is one launch (``add_rms_norm``) and the MLP's SiLU * up another
+(``silu_mul``); the ops after a split-K projection sum its partials, and every op keeps the
+reference ops' rounding.
 
 :class:`GraphDecoder` is the decode step with no host work per step: slot map, seqlen,
 RoPE rows, 28 layers, lm_head and the greedy argmax are captured once in a HIP graph and
@@ -32,6 +33,7 @@ from . import _lib
 from .decode import paged_decode_plan
 from .packed import PackedPrefill
 from .paged import PagedKV, PagedPool, PagedWriteSink
+from .rows import Parts, rows_linear, rows_supported
 
 __all__ = ["Qwen3Config", "random_weights", "Qwen3", "GraphDecoder"]
 
@@ -101,32 +103,44 @@ def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.T
     return torch.cat([x1 * cos - x2 * sin, x1 * sin + x2 * cos], dim=-1)
 
 
-def add_rms_norm(x: torch.Tensor, delta: torch.Tensor | None, weight: torch.Tensor, eps: float):
+def _proj_arg(t, rows: int, cols: int, dtype: torch.dtype, name: str):
+    """(pointer, parts) of a projection output given as a tensor or as split-K :class:`Parts`."""
+    if isinstance(t, Parts):
+        if t.shape != (rows, cols) or t.dtype != dtype:
+            raise ValueError(f"{name} must be ({rows}, {cols}) {dtype}, got partial sums {t.shape} {t.dtype}")
+        return t.data.data_ptr(), t.n_parts
+    if not t.is_contiguous() or tuple(t.shape) != (rows, cols) or t.dtype != dtype:
+        raise ValueError(f"{name} must be contiguous ({rows}, {cols}) {dtype}, got {tuple(t.shape)} {t.dtype}")
+    return t.data_ptr(), 0
+
+
+def add_rms_norm(x: torch.Tensor, delta, weight: torch.Tensor, eps: float):
     """``x + delta`` (in place into ``x``) and its RMSNorm in one HIP launch (``mi_add_rms_norm``),
     rounded op by op as :func:`rms_norm` and the residual add are; returns ``(x, h)``.
-    ``x``/``delta``: contiguous ``(rows, cols)``; ``delta`` None normalises ``x`` as is."""
+    ``x``: contiguous ``(rows, cols)``; ``delta``: the same, or the :class:`Parts` of the
+    projection that produces it, or None (normalise ``x`` as is)."""
     rows, cols = x.shape
-    for name, t in (("x", x), ("delta", delta)):
-        if t is not None and (not t.is_contiguous() or tuple(t.shape) != (rows, cols) or t.dtype != x.dtype):
-            raise ValueError(f"{name} must be contiguous ({rows}, {cols}) {x.dtype}, got {tuple(t.shape)} {t.dtype}")
+    _proj_arg(x, rows, cols, x.dtype, "x")
+    d_ptr, d_parts = (None, 0) if delta is None else _proj_arg(delta, rows, cols, x.dtype, "delta")
     if tuple(weight.shape) != (cols,) or weight.dtype != x.dtype:
         raise ValueError(f"weight must be ({cols},) {x.dtype}")
     h = torch.empty_like(x)
-    rc = _lib.lib.mi_add_rms_norm(x.data_ptr(), None if delta is None else delta.data_ptr(), weight.data_ptr(),
+    rc = _lib.lib.mi_add_rms_norm(x.data_ptr(), d_ptr, d_parts, weight.data_ptr(),
                                   x.data_ptr() if delta is not None else None, h.data_ptr(), rows, cols, float(eps),
                                   _lib.dtype_code(x.dtype), _lib.current_stream(x.device))
     _lib.check(rc, "add_rms_norm")
     return x, h
 
 
-def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
-    """``silu(gate) * up`` of a ``(rows, 2 * inter)`` ``[gate | up]`` projection in one HIP
-    launch (``mi_silu_mul``), rounded op by op as ``F.silu(g) * u`` is."""
+def silu_mul(gate_up) -> torch.Tensor:
+    """``silu(gate) * up`` of a ``(rows, 2 * inter)`` ``[gate | up]`` projection (a tensor or its
+    :class:`Parts`) in one HIP launch (``mi_silu_mul``), rounded op by op as ``F.silu(g) * u`` is."""
     rows, two = gate_up.shape
-    if two % 2 or not gate_up.is_contiguous():
-        raise ValueError(f"gate_up must be contiguous (rows, 2 * inter), got {tuple(gate_up.shape)}")
+    if two % 2:
+        raise ValueError(f"gate_up must be (rows, 2 * inter), got {tuple(gate_up.shape)}")
+    ptr, parts = _proj_arg(gate_up, rows, two, gate_up.dtype, "gate_up")
     out = torch.empty((rows, two // 2), dtype=gate_up.dtype, device=gate_up.device)
-    rc = _lib.lib.mi_silu_mul(gate_up.data_ptr(), out.data_ptr(), rows, two // 2, _lib.dtype_code(gate_up.dtype),
+    rc = _lib.lib.mi_silu_mul(ptr, parts, out.data_ptr(), rows, two // 2, _lib.dtype_code(gate_up.dtype),
                               _lib.current_stream(gate_up.device))
     _lib.check(rc, "silu_mul")
     return out
@@ -208,12 +222,26 @@ class Qwen3:
         _, h = add_rms_norm(x, None, self.w["l0.ln1"], c.eps)
         for i in range(c.n_layer):
             p = f"l{i}."
-            y = attend(i, F.linear(h, self.w[p + "wqkv"]))
-            _, h = add_rms_norm(x, F.linear(y, self.w[p + "wo"]), self.w[p + "ln2"], c.eps)
-            m = silu_mul(F.linear(h, self.w[p + "wgu"]))
+            y = attend(i, self._proj(h, self.w[p + "wqkv"]))
+            _, h = add_rms_norm(x, self._proj(y, self.w[p + "wo"]), self.w[p + "ln2"], c.eps)
+            m = silu_mul(self._proj(h, self.w[p + "wgu"]))
             nxt = self.w[f"l{i + 1}.ln1"] if i + 1 < c.n_layer else self.w["norm"]
-            _, h = add_rms_norm(x, F.linear(m, self.w[p + "wd"]), nxt, c.eps)
+            _, h = add_rms_norm(x, self._proj(m, self.w[p + "wd"]), nxt, c.eps)
         return h
+
+    @staticmethod
+    def _proj(h: torch.Tensor, w: torch.Tensor):
+        """A decode-step projection: the HIP rows GEMM (``rows_linear``; its output may be split-K
+        :class:`Parts` for the next op to sum) where it applies (up to 32 rows), else
+        ``F.linear``."""
+        return rows_linear(h, w) if rows_supported(h, w) else F.linear(h, w)
+
+    def _lm_head(self, h: torch.Tensor) -> torch.Tensor:
+        """Logits ``(B, vocab)`` of the final-norm rows (tied embedding), one HIP launch."""
+        w = self.w["embed"]
+        if rows_supported(h, w) and h.shape[1] <= 1024:
+            return rows_linear(h, w, n_split=1)
+        return F.linear(h, w)
 
     def decode(self, paged: PagedKV, tokens: torch.Tensor) -> torch.Tensor:
         """One decode step of every row (reference ``MiniLLM.forward`` decode-container
@@ -223,7 +251,7 @@ class Qwen3:
         x = F.embedding(tokens.view(-1), self.w["embed"])  # (B, C)
         B = x.shape[0]
 
-        def attend(i: int, qkv: torch.Tensor) -> torch.Tensor:
+        def attend(i: int, qkv) -> torch.Tensor:
             # q/k norm + RoPE + K/V write in one HIP launch (the reference's tensor ops + write)
             p = f"l{i}."
             q = paged.write_rope(i, qkv, self.w[p + "qn"], self.w[p + "kn"], self.cos, self.sin, c.eps)
@@ -231,7 +259,7 @@ class Qwen3:
 
         h = self._decode_stack(x, attend)
         paged.advance()
-        return F.linear(h, self.w["embed"])
+        return self._lm_head(h)
 
 
 class GraphDecoder:
@@ -277,13 +305,13 @@ class GraphDecoder:
         slots = self.table64.gather(1, (self.pos // bs).view(-1, 1)).view(-1) * bs + self.pos % bs
         x = F.embedding(self.tokens, m.w["embed"])  # (B, C)
 
-        def attend(i: int, qkv: torch.Tensor) -> torch.Tensor:
+        def attend(i: int, qkv) -> torch.Tensor:
             p = f"l{i}."
             q = self.pool.write_qk_norm_rope(i, slots, qkv, m.w[p + "qn"], m.w[p + "kn"], m.cos, m.sin,
                                              self.pos, c.eps)
             return self.plan.run(i, q).view(self.B, -1)
 
-        nxt = F.linear(m._decode_stack(x, attend), m.w["embed"]).argmax(-1)
+        nxt = m._lm_head(m._decode_stack(x, attend)).argmax(-1)
         self.history.index_copy_(1, self.step_idx, nxt.view(-1, 1))
         self.tokens.copy_(nxt)
         self.pos.add_(1)

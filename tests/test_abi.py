@@ -217,3 +217,21 @@ def test_schedule_rejects_unknown_kernels_and_head_dims():
 def test_schedule_rejects_empty_segments():
     host_cu = (ctypes.c_int32 * 3)(0, 5, 5)
     assert _lib.lib.mi_varlen_schedule(host_cu, 2, 16, 8, 128, 1, None, 0) == _lib.MI_ERR_INVALID
+
+
+def test_rows_gemm_split_choice_and_argument_checks():
+    split = _lib.lib.mi_rows_gemm_split
+    # one launch of >= 192 workgroups with at most two 64-k steps per wave at the Qwen3-0.6B
+    # decode projections; the lm_head (4748 column tiles) needs no split
+    assert [split(32, n, k) for n, k in [(4096, 1024), (1024, 2048), (6144, 1024), (1024, 3072)]] == [2, 8, 2, 6]
+    assert split(32, 151936, 1024) == 1
+    assert split(32, 64, 1000) == 0
+    gemm = _lib.lib.mi_rows_gemm
+    assert gemm(None, 1024, None, 1024, None, 64, None, 33, 64, 1024, 1, 2, None) == _lib.MI_ERR_INVALID
+    assert "M=33" in _lib.last_error()
+    assert gemm(None, 1024, None, 1024, None, 64, None, 4, 64, 1000, 1, 2, None) == _lib.MI_ERR_UNSUPPORTED
+    assert gemm(None, 2048, None, 2048, None, 64, None, 4, 64, 2048, 1, 2, None) == _lib.MI_ERR_UNSUPPORTED
+    assert "more than 1024" in _lib.last_error()
+    assert gemm(None, 1024, None, 1024, None, 64, None, 4, 64, 1024, 2, 2, None) == _lib.MI_ERR_INVALID
+    assert "NULL" in _lib.last_error()
+

@@ -1,0 +1,134 @@
+"""The decode-step rows GEMM (``mi_rows_gemm``, ``miattn.rows.rows_linear``) against a float64
+product of the same bf16/fp16 operands, and the ops that consume its split-K partial sums
+against the same ops fed the summed, rounded projection.
+
+``nn.Linear`` rounds an fp32-accumulated dot product once to the activation dtype; the kernel
+does the same with another fp32 summation order, so a plain output lies within one unit in
+the last place of the exactly rounded product, and the fp32 partial sums, added in float64,
+lie within fp32 accumulation error (K products) of the exact product. A consumer fed
+:class:`Parts` sums them in split order and rounds once before its op chain, which
+``Parts.value()`` restates in torch: the results are bit-identical.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from miattn import PagedPool
+from miattn.qwen3 import add_rms_norm, rope_table, silu_mul
+from miattn.rows import Parts, rows_linear, rows_supported
+
+pytestmark = pytest.mark.gpu
+
+
+def _operands(M, N, K, dtype, seed, lda=None):
+    g = torch.Generator().manual_seed(seed)
+    lda = lda or K
+    a_full = torch.randn(M, lda, generator=g).to(dtype).cuda()
+    w = (torch.randn(N, K, generator=g) * 0.05).to(dtype).cuda()
+    return a_full[:, :K], w
+
+
+@pytest.mark.parametrize(
+    "M,N,K,n_split,dtype",
+    [
+        (32, 4096, 1024, None, torch.bfloat16),   # q/k/v (stacked) at the Qwen3-0.6B shape
+        (32, 1024, 2048, None, torch.bfloat16),   # o_proj
+        (32, 6144, 1024, None, torch.bfloat16),   # gate/up (stacked)
+        (32, 1024, 3072, None, torch.bfloat16),   # down_proj
+        (32, 8208, 1024, 1, torch.bfloat16),      # lm_head-like, N not a multiple of 32 tiles of 1024
+        (5, 100, 1024, 1, torch.bfloat16),
+        (17, 1000, 2048, 4, torch.float16),
+        (1, 33, 256, 1, torch.bfloat16),
+        (3, 64, 3072, 12, torch.bfloat16),
+        (32, 4096, 1024, 1, torch.float16),
+        (31, 96, 512, 2, torch.bfloat16),
+    ],
+)
+def test_rows_gemm_matches_the_exact_product(M, N, K, n_split, dtype):
+    a, w = _operands(M, N, K, dtype, seed=M * 131 + N + K)
+    exact = a.double() @ w.double().t()
+    got = rows_linear(a, w, n_split=n_split)
+    torch.cuda.synchronize()
+    scale = exact.abs().max().item()
+    if isinstance(got, Parts):
+        assert n_split != 1 and got.shape == (M, N) and got.dtype == dtype
+        total = got.data.double().sum(0)
+        assert (total - exact).abs().max().item() <= 1e-5 * scale
+        got = got.value()
+    assert got.shape == (M, N) and got.dtype == dtype
+    # one ulp of the dtype at each element's magnitude (the exact product rounded once is
+    # within half an ulp; the fp32 sum order moves it by far less than the other half)
+    ulp = torch.finfo(dtype).eps * exact.abs().clamp(min=scale * 1e-3)
+    assert ((got.double() - exact).abs() <= ulp).all()
+
+
+def test_rows_gemm_row_strides_and_a_reused_output():
+    a, w = _operands(8, 256, 1024, torch.bfloat16, seed=5, lda=1024 + 64)
+    assert a.stride(0) == 1088
+    want = rows_linear(a.contiguous(), w, n_split=1)
+    for _ in range(2):
+        got = rows_linear(a, w, n_split=1)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want)
+
+
+def test_rows_linear_rejects_what_it_does_not_take():
+    w = torch.zeros(64, 1024, dtype=torch.bfloat16, device="cuda")
+    for bad_a in (torch.zeros(33, 1024, dtype=torch.bfloat16, device="cuda"),
+                  torch.zeros(4, 1000, dtype=torch.bfloat16, device="cuda"),
+                  torch.zeros(4, 1024, dtype=torch.float32, device="cuda")):
+        assert not rows_supported(bad_a, w)
+        with pytest.raises(ValueError, match="rows_linear"):
+            rows_linear(bad_a, w)
+    with pytest.raises(ValueError, match="n_split"):
+        rows_linear(torch.zeros(4, 1024, dtype=torch.bfloat16, device="cuda"), w, n_split=3)
+
+
+def _parts(M, N, S, dtype, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return Parts((torch.randn(S, M, N, generator=g) * scale).cuda(), dtype)
+
+
+@pytest.mark.parametrize("S", [2, 6])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_add_rms_norm_takes_partial_sums(S, dtype):
+    g = torch.Generator().manual_seed(S)
+    x = torch.randn(32, 1024, generator=g).to(dtype).cuda()
+    w = (1.0 + 0.1 * torch.randn(1024, generator=g)).to(dtype).cuda()
+    d = _parts(32, 1024, S, dtype, seed=S + 1)
+    x1, h1 = add_rms_norm(x.clone(), d, w, 1e-6)
+    x2, h2 = add_rms_norm(x.clone(), d.value(), w, 1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(x1, x2) and torch.equal(h1, h2)
+
+
+@pytest.mark.parametrize("S", [2, 4])
+def test_silu_mul_takes_partial_sums(S):
+    gu = _parts(32, 2 * 3072, S, torch.bfloat16, seed=7 + S, scale=2.0)
+    got = silu_mul(gu)
+    want = silu_mul(gu.value())
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("S", [1, 2])
+@pytest.mark.parametrize("B,H,H_kv,D", [(32, 16, 8, 128), (5, 8, 2, 256)])
+def test_epilogue_takes_partial_sums(S, B, H, H_kv, D):
+    dtype = torch.bfloat16
+    g = torch.Generator().manual_seed(B + D + S)
+    qkv = _parts(B, (H + 2 * H_kv) * D, S, dtype, seed=B * D + S, scale=2.0)
+    qn = (1.0 + 0.1 * torch.randn(D, generator=g)).to(dtype).cuda()
+    kn = (1.0 + 0.1 * torch.randn(D, generator=g)).to(dtype).cuda()
+    cos, sin = rope_table(D, 1e6, 4096, "cuda", dtype)
+    pos = torch.randint(0, 4096, (B,), generator=g).cuda()
+    slots = torch.randperm(64 * 16, generator=g)[:B].cuda()
+    pools = [PagedPool(1, 64, 16, H_kv, D, dtype=dtype, device="cuda", n_head=H, strict_writes=True)
+             for _ in range(2)]
+    q1 = pools[0].write_qk_norm_rope(0, slots, qkv, qn, kn, cos, sin, pos, 1e-6)
+    q2 = pools[1].write_qk_norm_rope(0, slots, qkv.value(), qn, kn, cos, sin, pos, 1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(q1, q2)
+    assert torch.equal(pools[0].keys[0], pools[1].keys[0])
+    assert torch.equal(pools[0].values[0], pools[1].values[0])
