@@ -118,6 +118,11 @@ int mi_add_rms_norm(const void* x, const void* delta, int delta_parts, const voi
 int mi_silu_mul(const void* gate_up, int gate_up_parts, void* out, int rows, int inter, int dtype,
                 void* stream);
 
+/* Greedy pick of the decode step (the reference's logits.argmax(-1) in its generate loop):
+ * out[r] = torch.argmax(x[r, :cols]) for each of `rows` rows of row stride ld -- the first
+ * index of the largest value, NaN above every number. out: int64 (rows,). */
+int mi_argmax_rows(const void* x, int64_t ld, int rows, int cols, int64_t* out, int dtype, void* stream);
+
 /* ------------------------------------------------------------------ decode-step projections
  * out = a w^T for 1 <= M <= 32 rows (nn.Linear without bias, the reference's projections at
  * decode batch = running sequences). a (M, K), w (N, K), both with unit element stride, row

@@ -72,6 +72,37 @@ __device__ __forceinline__ void store16(void* p, const uint4& v) {
   *reinterpret_cast<uint4*>(p) = v;
 }
 
+// Sum over s = 0 .. parts-1 (parts >= 1) of f[s * plane], added in that order in fp32 (the
+// split-K partial sums of one output element), split into a load and a sum step so a kernel
+// can issue the loads of all its elements before any arithmetic (an empty asm in a rounding
+// helper is a scheduling barrier the loads would otherwise not cross). kU > 0 needs
+// parts <= kU: kU loads with the index clamped to the last partial (always in bounds) and a
+// straight-line sum. kU = 0: a plain loop for any count, summed at load time.
+template <int kU>
+struct PartSum {
+  static constexpr int N = kU > 0 ? kU : 1;
+  float v[N];
+  __device__ __forceinline__ void load(const float* f, int parts, int64_t plane) {
+    if constexpr (kU == 0) {
+      float acc = f[0];
+      for (int s = 1; s < parts; ++s) acc += f[s * plane];
+      v[0] = acc;
+    } else {
+#pragma unroll
+      for (int s = 0; s < kU; ++s) v[s] = f[int64_t(s < parts ? s : parts - 1) * plane];
+    }
+  }
+  __device__ __forceinline__ float sum(int parts) const {
+    float acc = v[0];
+#pragma unroll
+    for (int s = 1; s < N; ++s) acc = s < parts ? acc + v[s] : acc;
+    return acc;
+  }
+};
+
+// Unroll class of PartSum for a partial count; -1: no partials (the input holds T values).
+constexpr int parts_unroll(int parts) { return parts == 0 ? -1 : (parts <= 2 ? 2 : (parts <= 8 ? 8 : 0)); }
+
 // 16-byte global load and store with the nontemporal (streaming) hint, for data that one
 // kernel touches once.
 typedef unsigned u32x4_nt __attribute__((ext_vector_type(4)));

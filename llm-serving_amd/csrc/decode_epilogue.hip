@@ -21,6 +21,8 @@
 // for p = l, l + 64, ... < D/2, so the pair partner is in the same lane. The projection
 // rows are T, or fp32 split-K partial sums [parts][B][row_stride] of mi_rows_gemm, summed
 // in split order and rounded once to T (the value the projection's own output would hold).
+#include <type_traits>
+
 #include "common.h"
 
 namespace miattn {
@@ -36,7 +38,7 @@ __device__ __forceinline__ float rt(float x) {
   return to_f32(from_f32<T>(x));
 }
 
-template <typename T, int D, typename IdxT>
+template <typename T, int D, typename IdxT, int kU>
 __global__ __launch_bounds__(256) void qk_norm_rope_write_kernel(
     const void* __restrict__ qkv, int64_t row_stride, int parts, int64_t plane, const T* __restrict__ q_w,
     const T* __restrict__ k_w,
@@ -60,20 +62,46 @@ __global__ __launch_bounds__(256) void qk_norm_rope_write_kernel(
     return;
   }
   const int64_t src = int64_t(b) * row_stride + int64_t(head) * D;
-  auto in = [&](int p) {
-    if (parts == 0) return to_f32(static_cast<const T*>(qkv)[src + p]);
-    const float* f = static_cast<const float*>(qkv) + src + p;
-    float acc = f[0];
-    for (int sp = 1; sp < parts; ++sp) acc += f[sp * plane];
-    return rt<T>(acc);
-  };
-
+  // every load of this wave's inputs first, then the arithmetic (the rounding helper's empty
+  // asm is a scheduling barrier)
+  constexpr int kP = kU < 0 ? 1 : kU;
+  PartSum<kP> r1[PPL], r2[PPL];
+#pragma unroll
+  for (int j = 0; j < PPL; ++j) {
+    const int p = min(lane + 64 * j, HALF - 1);
+    if constexpr (kU < 0) {
+      r1[j].v[0] = to_f32(static_cast<const T*>(qkv)[src + p]);
+      r2[j].v[0] = to_f32(static_cast<const T*>(qkv)[src + p + HALF]);
+    } else {
+      r1[j].load(static_cast<const float*>(qkv) + src + p, parts, plane);
+      r2[j].load(static_cast<const float*>(qkv) + src + p + HALF, parts, plane);
+    }
+  }
+  // norm weights and this row's RoPE table entries (read here, used after the reduction)
+  const bool is_q = head < H;
+  const T* w = is_q ? q_w : k_w;
+  const T* cr = cos_tab + pb * HALF;
+  const T* sr = sin_tab + pb * HALF;
+  float w1[PPL], w2[PPL], cs[PPL], sn[PPL];
+#pragma unroll
+  for (int j = 0; j < PPL; ++j) {
+    const int p = min(lane + 64 * j, HALF - 1);
+    w1[j] = to_f32(w[p]);
+    w2[j] = to_f32(w[p + HALF]);
+    cs[j] = to_f32(cr[p]);
+    sn[j] = to_f32(sr[p]);
+  }
   float x1[PPL], x2[PPL];
 #pragma unroll
   for (int j = 0; j < PPL; ++j) {
-    const int p = lane + 64 * j;
-    x1[j] = p < HALF ? in(p) : 0.0f;
-    x2[j] = p < HALF ? in(p + HALF) : 0.0f;
+    const bool live = lane + 64 * j < HALF;
+    if constexpr (kU < 0) {
+      x1[j] = live ? r1[j].v[0] : 0.0f;
+      x2[j] = live ? r2[j].v[0] : 0.0f;
+    } else {
+      x1[j] = live ? rt<T>(r1[j].sum(parts)) : 0.0f;
+      x2[j] = live ? rt<T>(r2[j].sum(parts)) : 0.0f;
+    }
   }
 
   if (head >= H + H_kv) {  // v head: copied as is (exact: x1/x2 hold T values)
@@ -90,8 +118,6 @@ __global__ __launch_bounds__(256) void qk_norm_rope_write_kernel(
   }
 
   // RMSNorm: mean of the rounded squares (fp32 sum), then the reference's rounding steps
-  const bool is_q = head < H;
-  const T* w = is_q ? q_w : k_w;
   float ss = 0.0f;
 #pragma unroll
   for (int j = 0; j < PPL; ++j) ss += rt<T>(x1[j] * x1[j]) + rt<T>(x2[j] * x2[j]);
@@ -99,18 +125,15 @@ __global__ __launch_bounds__(256) void qk_norm_rope_write_kernel(
   const float ms = rt<T>(ss * (1.0f / D));
   const float rms = rt<T>(sqrtf(rt<T>(ms + eps)));
   // RoPE at this row's position (table rows of D/2)
-  const T* cr = cos_tab + pb * HALF;
-  const T* sr = sin_tab + pb * HALF;
   float o1[PPL], o2[PPL];
 #pragma unroll
   for (int j = 0; j < PPL; ++j) {
     const int p = lane + 64 * j;
     if (p < HALF) {
-      const float a = rt<T>(rt<T>(x1[j] / rms) * to_f32(w[p]));
-      const float c = rt<T>(rt<T>(x2[j] / rms) * to_f32(w[p + HALF]));
-      const float cs = to_f32(cr[p]), sn = to_f32(sr[p]);
-      o1[j] = rt<T>(rt<T>(a * cs) - rt<T>(c * sn));
-      o2[j] = rt<T>(rt<T>(a * sn) + rt<T>(c * cs));
+      const float a = rt<T>(rt<T>(x1[j] / rms) * w1[j]);
+      const float c = rt<T>(rt<T>(x2[j] / rms) * w2[j]);
+      o1[j] = rt<T>(rt<T>(a * cs[j]) - rt<T>(c * sn[j]));
+      o2[j] = rt<T>(rt<T>(a * sn[j]) + rt<T>(c * cs[j]));
     }
   }
 
@@ -138,15 +161,23 @@ int launch_d(const void* qkv, int64_t row_stride, int parts, const void* q_w, co
   constexpr int kWaves = 4;
   const dim3 grid((H + 2 * H_kv + kWaves - 1) / kWaves, B);
   const int64_t plane = int64_t(B) * row_stride;
-  auto go = [&](auto idx_tag) {
+  auto go = [&](auto idx_tag, auto unroll) {
     using IdxT = decltype(idx_tag);
-    hipLaunchKernelGGL((qk_norm_rope_write_kernel<T, D, IdxT>), grid, dim3(64 * kWaves), 0, s, qkv,
+    hipLaunchKernelGGL((qk_norm_rope_write_kernel<T, D, IdxT, decltype(unroll)::value>), grid, dim3(64 * kWaves), 0, s, qkv,
                        row_stride, parts, plane, static_cast<const T*>(q_w), static_cast<const T*>(k_w),
                        static_cast<const T*>(cos_tab), static_cast<const T*>(sin_tab), n_pos, pos,
                        static_cast<const IdxT*>(slots), static_cast<T*>(q_out), static_cast<T*>(k_pool),
                        static_cast<T*>(v_pool), B, H, H_kv, n_slots, eps, err);
   };
-  if (slot_bits == 32) go(int32_t{}); else go(int64_t{});
+  auto by_slots = [&](auto unroll) {
+    if (slot_bits == 32) go(int32_t{}, unroll); else go(int64_t{}, unroll);
+  };
+  switch (parts_unroll(parts)) {
+    case -1: by_slots(std::integral_constant<int, -1>{}); break;
+    case 2: by_slots(std::integral_constant<int, 2>{}); break;
+    case 8: by_slots(std::integral_constant<int, 8>{}); break;
+    default: by_slots(std::integral_constant<int, 0>{}); break;
+  }
   return launch_status("mi_qk_norm_rope_write");
 }
 

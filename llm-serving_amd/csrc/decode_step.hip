@@ -18,6 +18,9 @@
 // may arrive as fp32 split-K partial sums [parts][rows][cols] of mi_rows_gemm: the op sums
 // them in split order and rounds once to the activation dtype, the value the projection's
 // own output would hold, before the chain above.
+#include <climits>
+#include <type_traits>
+
 #include "common.h"
 
 namespace miattn {
@@ -31,45 +34,66 @@ __device__ __forceinline__ float rnd(float x) {
   return to_f32(from_f32<T>(x));
 }
 
-// Element (row, col) of a projection output: T, or the rounded sum of fp32 partials.
-template <typename T>
+// Element (row, col) of a projection output: T, or the rounded sum of fp32 partials
+// (sum_parts<kU>).
+template <typename T, int kU>
 struct ProjIn {
   const void* p;
-  int parts;      // 0: p is T [rows][cols]; n >= 1: p is fp32 [n][rows][cols]
+  int parts;      // kU = -1: p is T [rows][cols]; else p is fp32 [parts][rows][cols]
   int64_t plane;  // rows * cols
-  __device__ __forceinline__ float at(int64_t idx) const {
-    if (parts == 0) return to_f32(static_cast<const T*>(p)[idx]);
-    const float* f = static_cast<const float*>(p);
-    float acc = f[idx];
-    for (int s = 1; s < parts; ++s) acc += f[s * plane + idx];
-    return rnd<T>(acc);
+  // Raw loads of element idx (issued first) ...
+  struct Raw {
+    PartSum<(kU < 0 ? 1 : kU)> ps;
+  };
+  __device__ __forceinline__ void load(int64_t idx, Raw& r) const {
+    if constexpr (kU < 0) {
+      r.ps.v[0] = to_f32(static_cast<const T*>(p)[idx]);
+    } else {
+      r.ps.load(static_cast<const float*>(p) + idx, parts, plane);
+    }
+  }
+  // ... and its value in T (the rounded sum of the partials).
+  __device__ __forceinline__ float value(const Raw& r) const {
+    if constexpr (kU < 0) {
+      return r.ps.v[0];
+    } else {
+      return rnd<T>(r.ps.sum(parts));
+    }
   }
 };
 
 constexpr int kNormThreads = 256;
 constexpr int kNormMaxPerThread = 16;  // rows of up to 4096 elements stay in registers
 
-// One workgroup per row: s = x + delta (or x), x_out = s, h_out = rmsnorm(s) * w.
-template <typename T, bool kAdd>
+// One workgroup per row: s = x + delta (or x), x_out = s, h_out = rmsnorm(s) * w. Each
+// thread holds PER elements (PER * 256 >= cols); every load of the row (x, w and all delta
+// partials) is issued before the first use, with indices past cols clamped to the row's last
+// element (loaded, never used).
+template <typename T, bool kAdd, int kU, int PER>
 __global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(
-    const T* x, ProjIn<T> delta, const T* __restrict__ w, T* x_out,  // x_out may alias x
+    const T* x, ProjIn<T, kU> delta, const T* __restrict__ w, T* x_out,  // x_out may alias x
     T* __restrict__ h_out, int cols, float eps) {
   __shared__ float part[kNormThreads / 64];
   const int64_t row = blockIdx.x;
   const int tid = threadIdx.x;
   const T* xr = x + row * cols;
-  float s[kNormMaxPerThread];
+  float s[PER], wv[PER];
+  typename ProjIn<T, kU>::Raw dr[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int ic = min(tid + j * kNormThreads, cols - 1);
+    s[j] = to_f32(xr[ic]);
+    wv[j] = to_f32(w[ic]);
+    if constexpr (kAdd) delta.load(row * cols + ic, dr[j]);
+  }
+  if constexpr (kAdd) {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) s[j] = rnd<T>(s[j] + delta.value(dr[j]));
+  }
   float ss = 0.0f;
 #pragma unroll
-  for (int j = 0; j < kNormMaxPerThread; ++j) {
-    const int i = tid + j * kNormThreads;
-    s[j] = 0.0f;
-    if (i < cols) {
-      float v = to_f32(xr[i]);
-      if constexpr (kAdd) v = rnd<T>(v + delta.at(row * cols + i));
-      s[j] = v;
-      ss += rnd<T>(v * v);
-    }
+  for (int j = 0; j < PER; ++j) {
+    if (tid + j * kNormThreads < cols) ss += rnd<T>(s[j] * s[j]);
   }
   ss = group_allreduce<64, SumOp>(ss);
   if ((tid & 63) == 0) part[tid >> 6] = ss;
@@ -80,50 +104,168 @@ __global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(
   const float ms = rnd<T>(total * (1.0f / float(cols)));  // the mean kernel scales by 1/N
   const float rms = rnd<T>(sqrtf(rnd<T>(ms + eps)));
 #pragma unroll
-  for (int j = 0; j < kNormMaxPerThread; ++j) {
+  for (int j = 0; j < PER; ++j) {
     const int i = tid + j * kNormThreads;
     if (i < cols) {
       if constexpr (kAdd) {
         if (x_out != nullptr) x_out[row * cols + i] = from_f32<T>(s[j]);
       }
-      h_out[row * cols + i] = from_f32<T>(rnd<T>(rnd<T>(s[j] / rms) * to_f32(w[i])));
+      h_out[row * cols + i] = from_f32<T>(rnd<T>(rnd<T>(s[j] / rms) * wv[j]));
     }
   }
 }
 
 // out[r, i] = silu(gu[r, i]) * gu[r, inter + i]
-template <typename T>
-__global__ __launch_bounds__(256) void silu_mul_kernel(ProjIn<T> gu, T* __restrict__ out, int inter) {
+template <typename T, int kU>
+__global__ __launch_bounds__(256) void silu_mul_kernel(ProjIn<T, kU> gu, T* __restrict__ out, int inter) {
   const int64_t row = blockIdx.y;
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= inter) return;
-  const float g = gu.at(row * 2 * inter + i);
-  const float u = gu.at(row * 2 * inter + inter + i);
+  typename ProjIn<T, kU>::Raw gr, ur;
+  gu.load(row * 2 * inter + i, gr);
+  gu.load(row * 2 * inter + inter + i, ur);
+  const float g = gu.value(gr);
+  const float u = gu.value(ur);
   const float sg = rnd<T>(g / (1.0f + expf(-g)));
   out[row * inter + i] = from_f32<T>(rnd<T>(sg * u));
 }
 
-template <typename T>
-int launch_norm(const void* x, const void* delta, int delta_parts, const void* w, void* x_out, void* h_out,
-                int rows, int cols, float eps, hipStream_t s) {
+template <typename T, int PER>
+int launch_norm_per(const void* x, const void* delta, int delta_parts, const void* w, void* x_out, void* h_out,
+                    int rows, int cols, float eps, hipStream_t s) {
   const dim3 grid(rows), block(kNormThreads);
-  const ProjIn<T> d{delta, delta_parts, int64_t(rows) * cols};
-  if (delta != nullptr) {
-    hipLaunchKernelGGL((add_rms_norm_kernel<T, true>), grid, block, 0, s, static_cast<const T*>(x), d,
-                       static_cast<const T*>(w), static_cast<T*>(x_out), static_cast<T*>(h_out), cols, eps);
+  const int64_t plane = int64_t(rows) * cols;
+  if (delta == nullptr) {
+    hipLaunchKernelGGL((add_rms_norm_kernel<T, false, -1, PER>), grid, block, 0, s, static_cast<const T*>(x),
+                       ProjIn<T, -1>{nullptr, 0, plane}, static_cast<const T*>(w), static_cast<T*>(nullptr),
+                       static_cast<T*>(h_out), cols, eps);
   } else {
-    hipLaunchKernelGGL((add_rms_norm_kernel<T, false>), grid, block, 0, s, static_cast<const T*>(x), d,
-                       static_cast<const T*>(w), static_cast<T*>(nullptr), static_cast<T*>(h_out), cols, eps);
+    auto go = [&](auto unroll) {
+      constexpr int U = decltype(unroll)::value;
+      hipLaunchKernelGGL((add_rms_norm_kernel<T, true, U, PER>), grid, block, 0, s, static_cast<const T*>(x),
+                         ProjIn<T, U>{delta, delta_parts, plane}, static_cast<const T*>(w), static_cast<T*>(x_out),
+                         static_cast<T*>(h_out), cols, eps);
+    };
+    switch (parts_unroll(delta_parts)) {
+      case -1: go(std::integral_constant<int, -1>{}); break;
+      case 2: go(std::integral_constant<int, 2>{}); break;
+      case 8: go(std::integral_constant<int, 8>{}); break;
+      default: go(std::integral_constant<int, 0>{}); break;
+    }
   }
   return launch_status("mi_add_rms_norm");
 }
 
 template <typename T>
+int launch_norm(const void* x, const void* delta, int delta_parts, const void* w, void* x_out, void* h_out,
+                int rows, int cols, float eps, hipStream_t s) {
+  if (cols <= 4 * kNormThreads) return launch_norm_per<T, 4>(x, delta, delta_parts, w, x_out, h_out, rows, cols, eps, s);
+  if (cols <= 8 * kNormThreads) return launch_norm_per<T, 8>(x, delta, delta_parts, w, x_out, h_out, rows, cols, eps, s);
+  return launch_norm_per<T, 16>(x, delta, delta_parts, w, x_out, h_out, rows, cols, eps, s);
+}
+
+template <typename T>
 int launch_silu(const void* gu, int gu_parts, void* out, int rows, int inter, hipStream_t s) {
   const dim3 grid((inter + 255) / 256, rows);
-  const ProjIn<T> g{gu, gu_parts, int64_t(rows) * 2 * inter};
-  hipLaunchKernelGGL((silu_mul_kernel<T>), grid, dim3(256), 0, s, g, static_cast<T*>(out), inter);
+  const int64_t plane = int64_t(rows) * 2 * inter;
+  auto go = [&](auto unroll) {
+    constexpr int U = decltype(unroll)::value;
+    hipLaunchKernelGGL((silu_mul_kernel<T, U>), grid, dim3(256), 0, s, ProjIn<T, U>{gu, gu_parts, plane},
+                       static_cast<T*>(out), inter);
+  };
+  switch (parts_unroll(gu_parts)) {
+    case -1: go(std::integral_constant<int, -1>{}); break;
+    case 2: go(std::integral_constant<int, 2>{}); break;
+    case 8: go(std::integral_constant<int, 8>{}); break;
+    default: go(std::integral_constant<int, 0>{}); break;
+  }
   return launch_status("mi_silu_mul");
+}
+
+// ---------------------------------------------------------------- greedy pick
+// torch.argmax over a row: the index of the largest value, the first one on ties, NaN above
+// every number (the first NaN wins).
+struct Best {
+  float v;
+  int i;
+};
+__device__ __forceinline__ bool better(float v, int i, const Best& b) {
+  const bool nv = v != v, nb = b.v != b.v;
+  if (nv != nb) return nv;
+  if (!nv && v != b.v) return v > b.v;
+  return i < b.i;
+}
+
+constexpr int kArgmaxThreads = 1024;
+
+// One workgroup per row; each thread walks 8-element (16-byte) pieces of the row 4 at a time
+// (all 4 loads in flight), then the workgroup reduces (value, index) pairs.
+template <typename T>
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_rows_kernel(const T* __restrict__ x, int64_t ld, int cols,
+                                                                     int64_t* __restrict__ out, bool vec) {
+  __shared__ Best part[kArgmaxThreads / 64];
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const T* xr = x + int64_t(row) * ld;
+  Best b{-INFINITY, INT_MAX};
+  if (vec) {
+    constexpr int E = 16 / int(sizeof(T));
+    constexpr int kUnroll = 4;
+    const int pieces = cols / E;
+    for (int p0 = tid; p0 < pieces; p0 += kArgmaxThreads * kUnroll) {
+      uint4 raw[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int pc = min(p0 + u * kArgmaxThreads, pieces - 1);
+        raw[u] = load16(xr + int64_t(pc) * E);
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int pc = p0 + u * kArgmaxThreads;
+        if (pc < pieces) {
+          const T* e = reinterpret_cast<const T*>(&raw[u]);
+#pragma unroll
+          for (int k = 0; k < E; ++k) {
+            const float v = to_f32(e[k]);
+            if (better(v, pc * E + k, b)) b = Best{v, pc * E + k};
+          }
+        }
+      }
+    }
+    for (int i = pieces * E + tid; i < cols; i += kArgmaxThreads) {  // tail past the last piece
+      const float v = to_f32(xr[i]);
+      if (better(v, i, b)) b = Best{v, i};
+    }
+  } else {
+    for (int i = tid; i < cols; i += kArgmaxThreads) {
+      const float v = to_f32(xr[i]);
+      if (better(v, i, b)) b = Best{v, i};
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(b.v, off, 64);
+    const int oi = __shfl_xor(b.i, off, 64);
+    if (better(ov, oi, b)) b = Best{ov, oi};
+  }
+  if ((tid & 63) == 0) part[tid >> 6] = b;
+  __syncthreads();
+  if (tid == 0) {
+    Best r = part[0];
+#pragma unroll
+    for (int k = 1; k < kArgmaxThreads / 64; ++k) {
+      if (better(part[k].v, part[k].i, r)) r = part[k];
+    }
+    out[row] = r.i;
+  }
+}
+
+template <typename T>
+int launch_argmax(const void* x, int64_t ld, int rows, int cols, int64_t* out, hipStream_t s) {
+  const bool vec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && (ld * int64_t(sizeof(T))) % 16 == 0;
+  hipLaunchKernelGGL((argmax_rows_kernel<T>), dim3(rows), dim3(kArgmaxThreads), 0, s, static_cast<const T*>(x), ld,
+                     cols, out, vec);
+  return launch_status("mi_argmax_rows");
 }
 
 }  // namespace
@@ -165,5 +307,22 @@ extern "C" int mi_silu_mul(const void* gate_up, int gate_up_parts, void* out, in
     case MI_F16: return launch_silu<f16_t>(gate_up, gate_up_parts, out, rows, inter, s);
     case MI_F32: return launch_silu<float>(gate_up, gate_up_parts, out, rows, inter, s);
     default: return fail(MI_ERR_INVALID, "mi_silu_mul: unknown dtype %d", dtype);
+  }
+}
+
+extern "C" int mi_argmax_rows(const void* x, int64_t ld, int rows, int cols, int64_t* out, int dtype, void* stream) {
+  using namespace miattn;
+  if (rows < 0 || cols < 1 || ld < cols) {
+    return fail(MI_ERR_INVALID, "mi_argmax_rows: bad shape rows=%d cols=%d ld=%lld", rows, cols, (long long)ld);
+  }
+  if (x == nullptr || out == nullptr) return fail(MI_ERR_INVALID, "mi_argmax_rows: NULL pointer");
+  if (rows == 0) return MI_OK;
+  if (rows > 2147483647) return fail(MI_ERR_UNSUPPORTED, "mi_argmax_rows: too many rows");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case MI_BF16: return launch_argmax<bf16_t>(x, ld, rows, cols, out, s);
+    case MI_F16: return launch_argmax<f16_t>(x, ld, rows, cols, out, s);
+    case MI_F32: return launch_argmax<float>(x, ld, rows, cols, out, s);
+    default: return fail(MI_ERR_INVALID, "mi_argmax_rows: unknown dtype %d", dtype);
   }
 }

@@ -33,7 +33,7 @@ from . import _lib
 from .decode import paged_decode_plan
 from .packed import PackedPrefill
 from .paged import PagedKV, PagedPool, PagedWriteSink
-from .rows import Parts, rows_linear, rows_supported
+from .rows import Parts, argmax_rows, rows_linear, rows_supported
 
 __all__ = ["Qwen3Config", "random_weights", "Qwen3", "GraphDecoder"]
 
@@ -311,7 +311,7 @@ class GraphDecoder:
                                              self.pos, c.eps)
             return self.plan.run(i, q).view(self.B, -1)
 
-        nxt = m._lm_head(m._decode_stack(x, attend)).argmax(-1)
+        nxt = argmax_rows(m._lm_head(m._decode_stack(x, attend)))
         self.history.index_copy_(1, self.step_idx, nxt.view(-1, 1))
         self.tokens.copy_(nxt)
         self.pos.add_(1)

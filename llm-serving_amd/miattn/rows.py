@@ -17,7 +17,7 @@ import torch
 
 from . import _lib
 
-__all__ = ["MAX_ROWS", "Parts", "rows_linear", "rows_supported", "split_for"]
+__all__ = ["MAX_ROWS", "Parts", "argmax_rows", "rows_linear", "rows_supported", "split_for"]
 
 MAX_ROWS = 32
 _K_UNIT = 256  # k per workgroup step: 4 waves x 64
@@ -103,3 +103,18 @@ def rows_linear(x: torch.Tensor, w: torch.Tensor, *, n_split: int | None = None)
                                M, N, K, S, code, stream)
     _lib.check(rc, "rows_linear")
     return Parts(part, x.dtype)
+
+
+def argmax_rows(x: torch.Tensor) -> torch.Tensor:
+    """``x.argmax(-1)`` of a 2-D HIP tensor (unit element stride) in one HIP launch
+    (``mi_argmax_rows``): int64 ``(rows,)``, the first index of each row's largest value, NaN
+    above every number -- torch's rule."""
+    _lib.require_library("argmax_rows")
+    if x.dim() != 2 or x.stride(1) != 1 or not x.is_cuda or x.shape[1] < 1:
+        raise ValueError(f"argmax_rows needs a 2-D HIP tensor with unit element stride, got {tuple(x.shape)}")
+    out = torch.empty(x.shape[0], dtype=torch.int64, device=x.device)
+    rc = _lib.lib.mi_argmax_rows(x.data_ptr(), x.stride(0), x.shape[0], x.shape[1], out.data_ptr(),
+                                 _lib.dtype_code(x.dtype), _lib.current_stream(x.device))
+    _lib.check(rc, "argmax_rows")
+    return out
+

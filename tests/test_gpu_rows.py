@@ -17,7 +17,7 @@ import torch
 
 from miattn import PagedPool
 from miattn.qwen3 import add_rms_norm, rope_table, silu_mul
-from miattn.rows import Parts, rows_linear, rows_supported
+from miattn.rows import Parts, argmax_rows, rows_linear, rows_supported
 
 pytestmark = pytest.mark.gpu
 
@@ -132,3 +132,29 @@ def test_epilogue_takes_partial_sums(S, B, H, H_kv, D):
     assert torch.equal(q1, q2)
     assert torch.equal(pools[0].keys[0], pools[1].keys[0])
     assert torch.equal(pools[0].values[0], pools[1].values[0])
+
+
+@pytest.mark.parametrize("rows,cols,dtype", [(32, 151936, torch.bfloat16), (3, 1000, torch.float16),
+                                             (5, 8193, torch.float32), (1, 7, torch.bfloat16)])
+def test_argmax_rows_is_torch_argmax(rows, cols, dtype):
+    g = torch.Generator().manual_seed(rows + cols)
+    x = torch.randn(rows, cols, generator=g).to(dtype)
+    # planted ties: two equal maxima (the first wins), a row of equal values, a NaN after a max
+    x[0, cols // 3] = 100.0
+    x[0, cols - 1] = 100.0
+    if rows > 1:
+        x[1] = 0.5
+    if rows > 2:
+        x[2, 0] = 50.0
+        x[2, cols // 2] = float("nan")
+        x[2, cols - 1] = float("nan")
+    got = argmax_rows(x.cuda())
+    torch.cuda.synchronize()
+    assert torch.equal(got.cpu(), x.argmax(-1))
+
+
+def test_argmax_rows_on_a_strided_view():
+    x = torch.randn(4, 300, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16)
+    view = x.cuda()[:, 5:290]  # rows 600 bytes apart, not 16-byte aligned: the scalar walk
+    assert torch.equal(argmax_rows(view).cpu(), x[:, 5:290].argmax(-1))
+
