@@ -136,6 +136,13 @@ int mi_argmax_rows(const void* x, int64_t ld, int rows, int cols, int64_t* out, 
 int mi_rows_gemm_split(int M, int N, int K);
 int mi_rows_gemm(const void* a, int64_t lda, const void* w, int64_t ldw, void* out, int64_t ldo,
                  float* partials, int M, int N, int K, int n_split, int dtype, void* stream);
+/* The MLP's first half in one launch: out (M, inter) = silu(a w_gate^T) * (a w_up^T), rounded
+ * as the reference's F.silu(gate(x)) * up(x) (model/layers.py:325-335). w_glu (2 * inter, K)
+ * holds the gate and up rows interleaved by 16: rows 32t .. 32t+15 are gate rows 16t .. 16t+15
+ * and rows 32t+16 .. 32t+31 are up rows 16t .. 16t+15. inter % 16 == 0, K % 256 == 0,
+ * K <= 1024 (unsplit), other requirements as mi_rows_gemm. */
+int mi_rows_gemm_glu(const void* a, int64_t lda, const void* w_glu, int64_t ldw, void* out, int64_t ldo,
+                     int M, int inter, int K, int dtype, void* stream);
 
 /* ------------------------------------------------------------------ paged decode
  * Replaces paged_decode (reference model/triton_decode.py:250-328) and its kernel

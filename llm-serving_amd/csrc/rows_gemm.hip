@@ -91,7 +91,20 @@ __device__ __forceinline__ void to_operands(uint4* __restrict__ lds, uint4 (&fra
 template <int NIT>
 constexpr bool stage_a() { return NIT <= 2; }
 
-template <typename T, int NIT>
+// Round an fp32 result to T behind an empty asm, so the compiler cannot fold the op and the
+// rounding into a native fp16 op of different rounding.
+template <typename T>
+__device__ __forceinline__ float round_t(float x) {
+  asm volatile("" : "+v"(x));
+  return to_f32(from_f32<T>(x));
+}
+
+// kGLU: W holds gate and up rows interleaved by 16 (column tile t = gate rows 16t..16t+15,
+// then up rows 16t..16t+15) and the launch is unsplit; the epilogue writes
+// out[i, 16t + c] = silu(g) * u with g, u the tile's columns c and 16 + c, rounded as the
+// reference's F.silu(gate(x)) * up(x) is: g and u to T, silu(g) = g / (1 + exp(-g)) in fp32 to
+// T, the product to T.
+template <typename T, int NIT, bool kGLU>
 __global__ __launch_bounds__(256) void rows_gemm_kernel(const T* __restrict__ a, int64_t lda,
                                                         const T* __restrict__ w, int64_t ldw,
                                                         T* __restrict__ out, int64_t ldo,
@@ -141,6 +154,24 @@ __global__ __launch_bounds__(256) void rows_gemm_kernel(const T* __restrict__ a,
 #pragma unroll
   for (int r = 0; r < 16; ++r) red[wave * kRedStride + r * 64 + lane] = acc[r];
   __syncthreads();
+  if constexpr (kGLU) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int h = q * 256 + tid;                         // 512 (row, gate column) pairs
+      const int r = h >> 5, ln = (h & 15) | ((h & 16) << 1);  // accumulator (r, lane), lane & 31 < 16
+      const int e = r * 64 + ln;
+      auto total = [&](int x) {
+        return ((red[x] + red[kRedStride + x]) + red[2 * kRedStride + x]) + red[3 * kRedStride + x];
+      };
+      const float g = round_t<T>(total(e));
+      const float u = round_t<T>(total(e + 16));
+      const float sg = round_t<T>(g / (1.0f + expf(-g)));
+      const int i = 8 * (r >> 2) + 4 * (ln >> 5) + (r & 3);
+      const int n = blockIdx.x * 16 + (ln & 15);
+      if (i < M) out[int64_t(i) * ldo + n] = from_f32<T>(round_t<T>(sg * u));
+    }
+    return;
+  }
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int e = q * 256 + tid;
@@ -158,7 +189,7 @@ __global__ __launch_bounds__(256) void rows_gemm_kernel(const T* __restrict__ a,
   }
 }
 
-template <typename T>
+template <typename T, bool kGLU>
 int launch_rows(const void* a, int64_t lda, const void* w, int64_t ldw, void* out, int64_t ldo, float* part,
                 int M, int N, int K, int S, int nit, hipStream_t s) {
   const dim3 grid((N + kTile - 1) / kTile, S), block(256);
@@ -166,12 +197,12 @@ int launch_rows(const void* a, int64_t lda, const void* w, int64_t ldw, void* ou
   const T* wt = static_cast<const T*>(w);
   T* ot = static_cast<T*>(out);
   switch (nit) {
-    case 1: hipLaunchKernelGGL((rows_gemm_kernel<T, 1>), grid, block, 0, s, at, lda, wt, ldw, ot, ldo, part, M, N, K); break;
-    case 2: hipLaunchKernelGGL((rows_gemm_kernel<T, 2>), grid, block, 0, s, at, lda, wt, ldw, ot, ldo, part, M, N, K); break;
-    case 3: hipLaunchKernelGGL((rows_gemm_kernel<T, 3>), grid, block, 0, s, at, lda, wt, ldw, ot, ldo, part, M, N, K); break;
-    default: hipLaunchKernelGGL((rows_gemm_kernel<T, 4>), grid, block, 0, s, at, lda, wt, ldw, ot, ldo, part, M, N, K); break;
+    case 1: hipLaunchKernelGGL((rows_gemm_kernel<T, 1, kGLU>), grid, block, 0, s, at, lda, wt, ldw, ot, ldo, part, M, N, K); break;
+    case 2: hipLaunchKernelGGL((rows_gemm_kernel<T, 2, kGLU>), grid, block, 0, s, at, lda, wt, ldw, ot, ldo, part, M, N, K); break;
+    case 3: hipLaunchKernelGGL((rows_gemm_kernel<T, 3, kGLU>), grid, block, 0, s, at, lda, wt, ldw, ot, ldo, part, M, N, K); break;
+    default: hipLaunchKernelGGL((rows_gemm_kernel<T, 4, kGLU>), grid, block, 0, s, at, lda, wt, ldw, ot, ldo, part, M, N, K); break;
   }
-  return launch_status("mi_rows_gemm");
+  return launch_status(kGLU ? "mi_rows_gemm_glu" : "mi_rows_gemm");
 }
 
 }  // namespace
@@ -226,8 +257,37 @@ extern "C" int mi_rows_gemm(const void* a, int64_t lda, const void* w, int64_t l
   float* part = n_split == 1 ? nullptr : partials;
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
-    case MI_BF16: return launch_rows<bf16_t>(a, lda, w, ldw, out, ldo, part, M, N, K, n_split, nit, s);
-    case MI_F16: return launch_rows<f16_t>(a, lda, w, ldw, out, ldo, part, M, N, K, n_split, nit, s);
+    case MI_BF16: return launch_rows<bf16_t, false>(a, lda, w, ldw, out, ldo, part, M, N, K, n_split, nit, s);
+    case MI_F16: return launch_rows<f16_t, false>(a, lda, w, ldw, out, ldo, part, M, N, K, n_split, nit, s);
     default: return fail(MI_ERR_UNSUPPORTED, "mi_rows_gemm: dtype %d (bf16 and fp16 only)", dtype);
+  }
+}
+
+extern "C" int mi_rows_gemm_glu(const void* a, int64_t lda, const void* w_glu, int64_t ldw, void* out, int64_t ldo,
+                                int M, int inter, int K, int dtype, void* stream) {
+  using namespace miattn;
+  if (M < 1 || M > kTile || inter < 1 || inter % 16 != 0 || K < 1) {
+    return fail(MI_ERR_INVALID, "mi_rows_gemm_glu: bad shape M=%d inter=%d K=%d (1 <= M <= %d, inter %% 16 == 0)", M,
+                inter, K, kTile);
+  }
+  if (K % (kGemmWaves * kStepK) != 0 || K / (kGemmWaves * kStepK) > 4) {
+    return fail(MI_ERR_UNSUPPORTED, "mi_rows_gemm_glu: K=%d must be a multiple of %d and at most %d", K,
+                kGemmWaves * kStepK, 4 * kGemmWaves * kStepK);
+  }
+  if (a == nullptr || w_glu == nullptr || out == nullptr) return fail(MI_ERR_INVALID, "mi_rows_gemm_glu: NULL pointer");
+  if (lda < K || ldw < K || ldo < inter) {
+    return fail(MI_ERR_INVALID, "mi_rows_gemm_glu: row strides (%lld, %lld, %lld) shorter than the rows",
+                (long long)lda, (long long)ldw, (long long)ldo);
+  }
+  if ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(w_glu)) % 16 != 0 || lda % 8 != 0 ||
+      ldw % 8 != 0) {
+    return fail(MI_ERR_UNSUPPORTED, "mi_rows_gemm_glu: A and W need 16-byte aligned rows");
+  }
+  const int nit = K / (kGemmWaves * kStepK);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case MI_BF16: return launch_rows<bf16_t, true>(a, lda, w_glu, ldw, out, ldo, nullptr, M, 2 * inter, K, 1, nit, s);
+    case MI_F16: return launch_rows<f16_t, true>(a, lda, w_glu, ldw, out, ldo, nullptr, M, 2 * inter, K, 1, nit, s);
+    default: return fail(MI_ERR_UNSUPPORTED, "mi_rows_gemm_glu: dtype %d (bf16 and fp16 only)", dtype);
   }
 }

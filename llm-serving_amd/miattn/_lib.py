@@ -78,6 +78,10 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "mi_silu_mul": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_int, _c_int, _c_int, _c_void_p]),
     "mi_rows_gemm_split": (_c_int, [_c_int, _c_int, _c_int]),
+    "mi_rows_gemm_glu": (
+        _c_int,
+        [_c_void_p, _c_int64, _c_void_p, _c_int64, _c_void_p, _c_int64, _c_int, _c_int, _c_int, _c_int, _c_void_p],
+    ),
     "mi_argmax_rows": (_c_int, [_c_void_p, _c_int64, _c_int, _c_int, _c_void_p, _c_int, _c_void_p]),
     "mi_rows_gemm": (
         _c_int,

@@ -33,7 +33,7 @@ from . import _lib
 from .decode import paged_decode_plan
 from .packed import PackedPrefill
 from .paged import PagedKV, PagedPool, PagedWriteSink
-from .rows import Parts, argmax_rows, rows_linear, rows_supported
+from .rows import Parts, argmax_rows, glu_weight, rows_linear, rows_supported, rows_swiglu
 
 __all__ = ["Qwen3Config", "random_weights", "Qwen3", "GraphDecoder"]
 
@@ -160,6 +160,8 @@ class Qwen3:
             p = f"l{i}."
             self.w[p + "wqkv"] = torch.cat([self.w[p + "wq"], self.w[p + "wk"], self.w[p + "wv"]], 0).contiguous()
             self.w[p + "wgu"] = torch.cat([self.w[p + "wg"], self.w[p + "wu"]], 0).contiguous()
+            # the same rows interleaved by 16 for the one-launch gate/up + SiLU * up
+            self.w[p + "wglu"] = glu_weight(self.w[p + "wg"], self.w[p + "wu"]).contiguous()
         self.dtype = self.w["embed"].dtype
         self.cos, self.sin = rope_table(cfg.head_dim, cfg.rope_theta, max_pos, self.device, self.dtype)
 
@@ -224,10 +226,18 @@ class Qwen3:
             p = f"l{i}."
             y = attend(i, self._proj(h, self.w[p + "wqkv"]))
             _, h = add_rms_norm(x, self._proj(y, self.w[p + "wo"]), self.w[p + "ln2"], c.eps)
-            m = silu_mul(self._proj(h, self.w[p + "wgu"]))
+            m = self._mlp_in(h, p)
             nxt = self.w[f"l{i + 1}.ln1"] if i + 1 < c.n_layer else self.w["norm"]
             _, h = add_rms_norm(x, self._proj(m, self.w[p + "wd"]), nxt, c.eps)
         return h
+
+    def _mlp_in(self, h: torch.Tensor, p: str) -> torch.Tensor:
+        """``silu(gate(h)) * up(h)``: one HIP launch (``rows_swiglu``) where it applies, else the
+        gate/up projection followed by ``silu_mul``."""
+        w = self.w[p + "wglu"]
+        if rows_supported(h, w) and h.shape[1] <= 1024:
+            return rows_swiglu(h, w)
+        return silu_mul(self._proj(h, self.w[p + "wgu"]))
 
     @staticmethod
     def _proj(h: torch.Tensor, w: torch.Tensor):

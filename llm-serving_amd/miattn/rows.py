@@ -17,7 +17,7 @@ import torch
 
 from . import _lib
 
-__all__ = ["MAX_ROWS", "Parts", "argmax_rows", "rows_linear", "rows_supported", "split_for"]
+__all__ = ["MAX_ROWS", "Parts", "argmax_rows", "glu_weight", "rows_linear", "rows_swiglu", "rows_supported", "split_for"]
 
 MAX_ROWS = 32
 _K_UNIT = 256  # k per workgroup step: 4 waves x 64
@@ -103,6 +103,36 @@ def rows_linear(x: torch.Tensor, w: torch.Tensor, *, n_split: int | None = None)
                                M, N, K, S, code, stream)
     _lib.check(rc, "rows_linear")
     return Parts(part, x.dtype)
+
+
+def glu_weight(w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:
+    """The ``(2 * inter, K)`` weight :func:`rows_swiglu` takes: gate and up rows interleaved by
+    16 (rows 32t..32t+15 = gate rows 16t..16t+15, rows 32t+16..32t+31 = up rows 16t..16t+15),
+    so each 32-column tile of the product holds matching gate and up columns."""
+    if w_gate.shape != w_up.shape or w_gate.dim() != 2 or w_gate.shape[0] % 16:
+        raise ValueError(f"gate/up weights must be equal (inter, K) with inter % 16 == 0, got "
+                         f"{tuple(w_gate.shape)} / {tuple(w_up.shape)}")
+    inter, K = w_gate.shape
+    return torch.stack([w_gate.view(inter // 16, 16, K), w_up.view(inter // 16, 16, K)], 1).reshape(2 * inter, K)
+
+
+def rows_swiglu(x: torch.Tensor, w_glu: torch.Tensor) -> torch.Tensor:
+    """``F.silu(x @ w_gate.T) * (x @ w_up.T)`` for 1-32 rows in one HIP launch
+    (``mi_rows_gemm_glu``), ``w_glu`` from :func:`glu_weight`; rounded as the reference's
+    ``F.silu(gate(x)) * up(x)`` is (each projection, the SiLU and the product to ``x.dtype``)."""
+    _lib.require_library("rows_swiglu")
+    if not rows_supported(x, w_glu) or x.shape[1] > 4 * _K_UNIT or w_glu.shape[0] % 32:
+        raise ValueError(
+            f"rows_swiglu needs x (M <= {MAX_ROWS}, K <= {4 * _K_UNIT}, K % {_K_UNIT} == 0) and w_glu "
+            f"(2 * inter, K) with inter % 16 == 0; got x {tuple(x.shape)} {x.dtype}, w {tuple(w_glu.shape)}"
+        )
+    M, K = x.shape
+    inter = int(w_glu.shape[0]) // 2
+    out = torch.empty((M, inter), dtype=x.dtype, device=x.device)
+    rc = _lib.lib.mi_rows_gemm_glu(x.data_ptr(), x.stride(0), w_glu.data_ptr(), w_glu.stride(0), out.data_ptr(),
+                                   inter, M, inter, K, _lib.dtype_code(x.dtype), _lib.current_stream(x.device))
+    _lib.check(rc, "rows_swiglu")
+    return out
 
 
 def argmax_rows(x: torch.Tensor) -> torch.Tensor:

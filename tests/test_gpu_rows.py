@@ -16,8 +16,10 @@ import pytest
 import torch
 
 from miattn import PagedPool
+import torch.nn.functional as F
+
 from miattn.qwen3 import add_rms_norm, rope_table, silu_mul
-from miattn.rows import Parts, argmax_rows, rows_linear, rows_supported
+from miattn.rows import Parts, argmax_rows, glu_weight, rows_linear, rows_supported, rows_swiglu
 
 pytestmark = pytest.mark.gpu
 
@@ -157,4 +159,32 @@ def test_argmax_rows_on_a_strided_view():
     x = torch.randn(4, 300, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16)
     view = x.cuda()[:, 5:290]  # rows 600 bytes apart, not 16-byte aligned: the scalar walk
     assert torch.equal(argmax_rows(view).cpu(), x[:, 5:290].argmax(-1))
+
+
+@pytest.mark.parametrize("M,inter,K,dtype", [(32, 3072, 1024, torch.bfloat16), (7, 48, 512, torch.float16),
+                                             (1, 16, 256, torch.bfloat16)])
+def test_swiglu_launch_equals_projection_then_silu_mul(M, inter, K, dtype):
+    g = torch.Generator().manual_seed(M + inter)
+    x = torch.randn(M, K, generator=g).to(dtype).cuda()
+    wg = (torch.randn(inter, K, generator=g) * 0.05).to(dtype).cuda()
+    wu = (torch.randn(inter, K, generator=g) * 0.05).to(dtype).cuda()
+    got = rows_swiglu(x, glu_weight(wg, wu))
+    # the same dot products through the plain launch, then the separate SiLU * up op
+    want = silu_mul(rows_linear(x, torch.cat([wg, wu], 0), n_split=1))
+    exact_g = (x.double() @ wg.double().t()).to(dtype)
+    exact_u = (x.double() @ wu.double().t()).to(dtype)
+    ref = F.silu(exact_g) * exact_u  # the reference's ops on correctly rounded projections
+    torch.cuda.synchronize()
+    assert got.shape == (M, inter) and got.dtype == dtype
+    assert torch.equal(got, want)
+    # within the projections' own rounding of the op chain on exactly rounded projections
+    assert ((got.float() - ref.float()).abs() <= 0.02 * ref.float().abs() + 1e-3).all()
+
+
+def test_glu_weight_interleaves_by_16():
+    wg = torch.arange(32 * 4, dtype=torch.float32).view(32, 4)
+    wu = -wg
+    w = glu_weight(wg, wu)
+    assert torch.equal(w[0:16], wg[0:16]) and torch.equal(w[16:32], wu[0:16])
+    assert torch.equal(w[32:48], wg[16:32]) and torch.equal(w[48:64], wu[16:32])
 
