@@ -123,6 +123,25 @@ int mi_silu_mul(const void* gate_up, int gate_up_parts, void* out, int rows, int
  * index of the largest value, NaN above every number. out: int64 (rows,). */
 int mi_argmax_rows(const void* x, int64_t ld, int rows, int cols, int64_t* out, int dtype, void* stream);
 
+/* The rest of a captured greedy decode step's bookkeeping, so the step needs no tensor ops
+ * (reference: the slot map model/paged.py:474-501, the embedding lookup and layer 0's input
+ * norm model/minillm.py:111-136, model/layers.py:342-350, the generate loop's argmax and
+ * position advance).
+ * mi_decode_step_begin, per row b (block_table (B, >= max_blocks) int32, row stride bt_stride):
+ *   seqlen[b] = pos[b] + 1;  slots[b] = table[b, pos[b] / block_size] * block_size + pos[b] % block_size;
+ *   x[b] = embed[tokens[b]] (embed (vocab, cols));  h[b] = x[b] / sqrt(mean(x[b]^2) + eps) * norm_w,
+ *   rounded as mi_add_rms_norm. A row whose token is outside [0, vocab) or whose position is
+ *   outside its table is not written and 1 + its index goes to *error_word (may be NULL).
+ * mi_greedy_advance: pick[r] = argmax of logits row r as mi_argmax_rows; tokens[r] = pick;
+ *   history[r * hist_stride + steps[r]] = pick while 0 <= steps[r] < max_steps; steps[r] += 1;
+ *   pos[r] += 1 (all int64). */
+int mi_decode_step_begin(const int64_t* tokens, const int64_t* pos, const int32_t* block_table, int64_t bt_stride,
+                         int block_size, int max_blocks, const void* embed, int64_t vocab, const void* norm_w,
+                         int cols, float eps, int32_t* seqlen, int64_t* slots, void* x, void* h, int B, int dtype,
+                         int32_t* error_word, void* stream);
+int mi_greedy_advance(const void* logits, int64_t ld, int rows, int cols, int dtype, int64_t* tokens, int64_t* pos,
+                      int64_t* history, int64_t hist_stride, int64_t* steps, int max_steps, void* stream);
+
 /* ------------------------------------------------------------------ decode-step projections
  * out = a w^T for 1 <= M <= 32 rows (nn.Linear without bias, the reference's projections at
  * decode batch = running sequences). a (M, K), w (N, K), both with unit element stride, row

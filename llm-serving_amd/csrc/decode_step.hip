@@ -65,31 +65,14 @@ struct ProjIn {
 constexpr int kNormThreads = 256;
 constexpr int kNormMaxPerThread = 16;  // rows of up to 4096 elements stay in registers
 
-// One workgroup per row: s = x + delta (or x), x_out = s, h_out = rmsnorm(s) * w. Each
-// thread holds PER elements (PER * 256 >= cols); every load of the row (x, w and all delta
-// partials) is issued before the first use, with indices past cols clamped to the row's last
-// element (loaded, never used).
-template <typename T, bool kAdd, int kU, int PER>
-__global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(
-    const T* x, ProjIn<T, kU> delta, const T* __restrict__ w, T* x_out,  // x_out may alias x
-    T* __restrict__ h_out, int cols, float eps) {
+// RMSNorm of one row held by a workgroup (PER elements per thread, PER * 256 >= cols; s and
+// the norm weights wv already loaded): h_row = s / sqrt(mean(s^2) + eps) * w, rounded step by
+// step, and x_row = s when x_row is not null.
+template <typename T, int PER>
+__device__ __forceinline__ void norm_row(const float (&s)[PER], const float (&wv)[PER], int cols, float eps,
+                                         T* x_row, T* __restrict__ h_row) {
   __shared__ float part[kNormThreads / 64];
-  const int64_t row = blockIdx.x;
   const int tid = threadIdx.x;
-  const T* xr = x + row * cols;
-  float s[PER], wv[PER];
-  typename ProjIn<T, kU>::Raw dr[PER];
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const int ic = min(tid + j * kNormThreads, cols - 1);
-    s[j] = to_f32(xr[ic]);
-    wv[j] = to_f32(w[ic]);
-    if constexpr (kAdd) delta.load(row * cols + ic, dr[j]);
-  }
-  if constexpr (kAdd) {
-#pragma unroll
-    for (int j = 0; j < PER; ++j) s[j] = rnd<T>(s[j] + delta.value(dr[j]));
-  }
   float ss = 0.0f;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
@@ -107,12 +90,71 @@ __global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(
   for (int j = 0; j < PER; ++j) {
     const int i = tid + j * kNormThreads;
     if (i < cols) {
-      if constexpr (kAdd) {
-        if (x_out != nullptr) x_out[row * cols + i] = from_f32<T>(s[j]);
-      }
-      h_out[row * cols + i] = from_f32<T>(rnd<T>(rnd<T>(s[j] / rms) * wv[j]));
+      if (x_row != nullptr) x_row[i] = from_f32<T>(s[j]);
+      h_row[i] = from_f32<T>(rnd<T>(rnd<T>(s[j] / rms) * wv[j]));
     }
   }
+}
+
+// One workgroup per row: s = x + delta (or x), x_out = s, h_out = rmsnorm(s) * w. Every load
+// of the row (x, w and all delta partials) is issued before the first use, with indices past
+// cols clamped to the row's last element (loaded, never used).
+template <typename T, bool kAdd, int kU, int PER>
+__global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(
+    const T* x, ProjIn<T, kU> delta, const T* __restrict__ w, T* x_out,  // x_out may alias x
+    T* __restrict__ h_out, int cols, float eps) {
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const T* xr = x + row * cols;
+  float s[PER], wv[PER];
+  typename ProjIn<T, kU>::Raw dr[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int ic = min(tid + j * kNormThreads, cols - 1);
+    s[j] = to_f32(xr[ic]);
+    wv[j] = to_f32(w[ic]);
+    if constexpr (kAdd) delta.load(row * cols + ic, dr[j]);
+  }
+  if constexpr (kAdd) {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) s[j] = rnd<T>(s[j] + delta.value(dr[j]));
+  }
+  T* x_row = (kAdd && x_out != nullptr) ? x_out + row * cols : nullptr;
+  norm_row<T, PER>(s, wv, cols, eps, x_row, h_out + row * cols);
+}
+
+// Start of a captured decode step, one workgroup per row: seqlen = pos + 1, the row's write
+// slot table[pos / bs] * bs + pos % bs (reference model/paged.py:499-501), x = embed[token]
+// (the embedding lookup) and h = rmsnorm(x) * w (layer 0's input norm). A row whose token is
+// outside the vocabulary or whose position is outside its block table is left unwritten
+// and reported (row + 1) through the error word.
+template <typename T, int PER>
+__global__ __launch_bounds__(kNormThreads) void step_begin_kernel(
+    const int64_t* __restrict__ tokens, const int64_t* __restrict__ pos, const int32_t* __restrict__ table,
+    int64_t bt_stride, int block_size, int max_blocks, const T* __restrict__ embed, int64_t vocab,
+    const T* __restrict__ w, int cols, float eps, int32_t* __restrict__ seqlen, int64_t* __restrict__ slots,
+    T* __restrict__ x, T* __restrict__ h, int32_t* __restrict__ err) {
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t t = tokens[row];
+  const int64_t p = pos[row];
+  if (t < 0 || t >= vocab || p < 0 || p / block_size >= max_blocks) {  // uniform over the workgroup
+    if (tid == 0 && err != nullptr) atomicCAS(err, 0, row + 1);
+    return;
+  }
+  if (tid == 0) {
+    seqlen[row] = int32_t(p + 1);
+    slots[row] = int64_t(table[row * bt_stride + p / block_size]) * block_size + p % block_size;
+  }
+  const T* er = embed + t * cols;
+  float s[PER], wv[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int ic = min(tid + j * kNormThreads, cols - 1);
+    s[j] = to_f32(er[ic]);
+    wv[j] = to_f32(w[ic]);
+  }
+  norm_row<T, PER>(s, wv, cols, eps, x + int64_t(row) * cols, h + int64_t(row) * cols);
 }
 
 // out[r, i] = silu(gu[r, i]) * gu[r, inter + i]
@@ -198,11 +240,22 @@ __device__ __forceinline__ bool better(float v, int i, const Best& b) {
 
 constexpr int kArgmaxThreads = 1024;
 
+// Optional end of a greedy decode step (all null: plain argmax): tokens[r] = pick,
+// history[r, steps[r]] = pick while steps[r] < max_steps, steps[r] += 1, pos[r] += 1.
+struct Advance {
+  int64_t* tokens;
+  int64_t* pos;
+  int64_t* history;
+  int64_t hist_stride;
+  int64_t* steps;
+  int max_steps;
+};
+
 // One workgroup per row; each thread walks 8-element (16-byte) pieces of the row 4 at a time
 // (all 4 loads in flight), then the workgroup reduces (value, index) pairs.
 template <typename T>
 __global__ __launch_bounds__(kArgmaxThreads) void argmax_rows_kernel(const T* __restrict__ x, int64_t ld, int cols,
-                                                                     int64_t* __restrict__ out, bool vec) {
+                                                                     int64_t* __restrict__ out, bool vec, Advance adv) {
   __shared__ Best part[kArgmaxThreads / 64];
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
@@ -256,16 +309,39 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_rows_kernel(const T* __
     for (int k = 1; k < kArgmaxThreads / 64; ++k) {
       if (better(part[k].v, part[k].i, r)) r = part[k];
     }
-    out[row] = r.i;
+    if (out != nullptr) out[row] = r.i;
+    if (adv.tokens != nullptr) {
+      adv.tokens[row] = r.i;
+      const int64_t st = adv.steps[row];
+      if (st >= 0 && st < adv.max_steps) adv.history[row * adv.hist_stride + st] = r.i;
+      adv.steps[row] = st + 1;
+      adv.pos[row] += 1;
+    }
   }
 }
 
 template <typename T>
-int launch_argmax(const void* x, int64_t ld, int rows, int cols, int64_t* out, hipStream_t s) {
+int launch_argmax(const void* x, int64_t ld, int rows, int cols, int64_t* out, const Advance& adv, hipStream_t s) {
   const bool vec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && (ld * int64_t(sizeof(T))) % 16 == 0;
   hipLaunchKernelGGL((argmax_rows_kernel<T>), dim3(rows), dim3(kArgmaxThreads), 0, s, static_cast<const T*>(x), ld,
-                     cols, out, vec);
-  return launch_status("mi_argmax_rows");
+                     cols, out, vec, adv);
+  return launch_status(adv.tokens != nullptr ? "mi_greedy_advance" : "mi_argmax_rows");
+}
+
+template <typename T>
+int launch_begin(const int64_t* tokens, const int64_t* pos, const int32_t* table, int64_t bt_stride, int block_size,
+                 int max_blocks, const void* embed, int64_t vocab, const void* w, int cols, float eps, int32_t* seqlen,
+                 int64_t* slots, void* x, void* h, int B, int32_t* err, hipStream_t s) {
+  auto go = [&](auto per) {
+    constexpr int PER = decltype(per)::value;
+    hipLaunchKernelGGL((step_begin_kernel<T, PER>), dim3(B), dim3(kNormThreads), 0, s, tokens, pos, table, bt_stride,
+                       block_size, max_blocks, static_cast<const T*>(embed), vocab, static_cast<const T*>(w), cols,
+                       eps, seqlen, slots, static_cast<T*>(x), static_cast<T*>(h), err);
+  };
+  if (cols <= 4 * kNormThreads) go(std::integral_constant<int, 4>{});
+  else if (cols <= 8 * kNormThreads) go(std::integral_constant<int, 8>{});
+  else go(std::integral_constant<int, 16>{});
+  return launch_status("mi_decode_step_begin");
 }
 
 }  // namespace
@@ -320,9 +396,63 @@ extern "C" int mi_argmax_rows(const void* x, int64_t ld, int rows, int cols, int
   if (rows > 2147483647) return fail(MI_ERR_UNSUPPORTED, "mi_argmax_rows: too many rows");
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
-    case MI_BF16: return launch_argmax<bf16_t>(x, ld, rows, cols, out, s);
-    case MI_F16: return launch_argmax<f16_t>(x, ld, rows, cols, out, s);
-    case MI_F32: return launch_argmax<float>(x, ld, rows, cols, out, s);
+    case MI_BF16: return launch_argmax<bf16_t>(x, ld, rows, cols, out, Advance{}, s);
+    case MI_F16: return launch_argmax<f16_t>(x, ld, rows, cols, out, Advance{}, s);
+    case MI_F32: return launch_argmax<float>(x, ld, rows, cols, out, Advance{}, s);
     default: return fail(MI_ERR_INVALID, "mi_argmax_rows: unknown dtype %d", dtype);
+  }
+}
+
+extern "C" int mi_greedy_advance(const void* logits, int64_t ld, int rows, int cols, int dtype, int64_t* tokens,
+                                 int64_t* pos, int64_t* history, int64_t hist_stride, int64_t* steps, int max_steps,
+                                 void* stream) {
+  using namespace miattn;
+  if (rows < 0 || cols < 1 || ld < cols || max_steps < 0 || hist_stride < max_steps) {
+    return fail(MI_ERR_INVALID, "mi_greedy_advance: bad shape rows=%d cols=%d ld=%lld max_steps=%d", rows, cols,
+                (long long)ld, max_steps);
+  }
+  if (logits == nullptr || tokens == nullptr || pos == nullptr || steps == nullptr ||
+      (max_steps > 0 && history == nullptr)) {
+    return fail(MI_ERR_INVALID, "mi_greedy_advance: NULL pointer");
+  }
+  if (rows == 0) return MI_OK;
+  const Advance adv{tokens, pos, history, hist_stride, steps, max_steps};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case MI_BF16: return launch_argmax<bf16_t>(logits, ld, rows, cols, nullptr, adv, s);
+    case MI_F16: return launch_argmax<f16_t>(logits, ld, rows, cols, nullptr, adv, s);
+    case MI_F32: return launch_argmax<float>(logits, ld, rows, cols, nullptr, adv, s);
+    default: return fail(MI_ERR_INVALID, "mi_greedy_advance: unknown dtype %d", dtype);
+  }
+}
+
+extern "C" int mi_decode_step_begin(const int64_t* tokens, const int64_t* pos, const int32_t* block_table,
+                                    int64_t bt_stride, int block_size, int max_blocks, const void* embed,
+                                    int64_t vocab, const void* norm_w, int cols, float eps, int32_t* seqlen,
+                                    int64_t* slots, void* x, void* h, int B, int dtype, int32_t* error_word,
+                                    void* stream) {
+  using namespace miattn;
+  if (B < 0 || cols < 1 || block_size < 1 || max_blocks < 1 || vocab < 1 || bt_stride < max_blocks) {
+    return fail(MI_ERR_INVALID, "mi_decode_step_begin: bad shape B=%d cols=%d block_size=%d max_blocks=%d", B, cols,
+                block_size, max_blocks);
+  }
+  if (cols > kNormThreads * kNormMaxPerThread) {
+    return fail(MI_ERR_UNSUPPORTED, "mi_decode_step_begin: rows of at most %d elements, got %d",
+                kNormThreads * kNormMaxPerThread, cols);
+  }
+  if (tokens == nullptr || pos == nullptr || block_table == nullptr || embed == nullptr || norm_w == nullptr ||
+      seqlen == nullptr || slots == nullptr || x == nullptr || h == nullptr) {
+    return fail(MI_ERR_INVALID, "mi_decode_step_begin: NULL pointer");
+  }
+  if (B == 0) return MI_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case MI_BF16: return launch_begin<bf16_t>(tokens, pos, block_table, bt_stride, block_size, max_blocks, embed,
+                                              vocab, norm_w, cols, eps, seqlen, slots, x, h, B, error_word, s);
+    case MI_F16: return launch_begin<f16_t>(tokens, pos, block_table, bt_stride, block_size, max_blocks, embed,
+                                            vocab, norm_w, cols, eps, seqlen, slots, x, h, B, error_word, s);
+    case MI_F32: return launch_begin<float>(tokens, pos, block_table, bt_stride, block_size, max_blocks, embed,
+                                            vocab, norm_w, cols, eps, seqlen, slots, x, h, B, error_word, s);
+    default: return fail(MI_ERR_INVALID, "mi_decode_step_begin: unknown dtype %d", dtype);
   }
 }

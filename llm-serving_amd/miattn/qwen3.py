@@ -146,6 +146,52 @@ def silu_mul(gate_up) -> torch.Tensor:
     return out
 
 
+def decode_step_begin(tokens: torch.Tensor, pos: torch.Tensor, table: torch.Tensor, block_size: int,
+                      embed: torch.Tensor, norm_w: torch.Tensor, eps: float, seqlen: torch.Tensor,
+                      slots: torch.Tensor, x: torch.Tensor, h: torch.Tensor, error: torch.Tensor) -> None:
+    """One HIP launch (``mi_decode_step_begin``) for the start of a decode step, in place:
+    ``seqlen = pos + 1`` (int32), ``slots = table[pos // bs] * bs + pos % bs`` (int64),
+    ``x = embed[tokens]`` and ``h = rms_norm(x, norm_w)``. A row with an out-of-range token or
+    position is left unwritten and reported through ``error`` (int32, row + 1)."""
+    B = tokens.numel()
+    V, C = embed.shape
+    for name, t, dt in (("tokens", tokens, torch.int64), ("pos", pos, torch.int64), ("slots", slots, torch.int64),
+                        ("seqlen", seqlen, torch.int32), ("error", error, torch.int32)):
+        if t.dtype != dt or not t.is_contiguous() or (name != "error" and t.numel() != B):
+            raise ValueError(f"{name} must be a contiguous {dt} tensor of {B} rows")
+    if table.dtype != torch.int32 or table.dim() != 2 or table.shape[0] != B or table.stride(1) != 1:
+        raise ValueError("table must be an int32 (B, max_blocks) block table with contiguous rows")
+    for name, t in (("x", x), ("h", h)):
+        if tuple(t.shape) != (B, C) or t.dtype != embed.dtype or not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous ({B}, {C}) {embed.dtype}")
+    if tuple(norm_w.shape) != (C,) or norm_w.dtype != embed.dtype or not embed.is_contiguous():
+        raise ValueError(f"norm_w must be ({C},) {embed.dtype} and embed contiguous")
+    rc = _lib.lib.mi_decode_step_begin(
+        tokens.data_ptr(), pos.data_ptr(), table.data_ptr(), table.stride(0), block_size, table.shape[1],
+        embed.data_ptr(), V, norm_w.data_ptr(), C, float(eps), seqlen.data_ptr(), slots.data_ptr(), x.data_ptr(),
+        h.data_ptr(), B, _lib.dtype_code(embed.dtype), error.data_ptr(), _lib.current_stream(x.device))
+    _lib.check(rc, "decode_step_begin")
+
+
+def greedy_advance(logits: torch.Tensor, tokens: torch.Tensor, pos: torch.Tensor, history: torch.Tensor,
+                   steps: torch.Tensor) -> None:
+    """One HIP launch (``mi_greedy_advance``) for the end of a greedy decode step, in place:
+    ``tokens = logits.argmax(-1)``, ``history[r, steps[r]] = tokens[r]`` while ``steps[r]`` is
+    inside ``history``, ``steps += 1``, ``pos += 1`` (all int64)."""
+    B, V = logits.shape
+    if logits.stride(1) != 1:
+        raise ValueError("logits must have unit element stride")
+    for name, t in (("tokens", tokens), ("pos", pos), ("steps", steps)):
+        if t.dtype != torch.int64 or t.numel() != B or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous int64 tensor of {B} rows")
+    if history.dtype != torch.int64 or history.dim() != 2 or history.shape[0] != B or history.stride(1) != 1:
+        raise ValueError(f"history must be an int64 ({B}, max_steps) tensor with contiguous rows")
+    rc = _lib.lib.mi_greedy_advance(logits.data_ptr(), logits.stride(0), B, V, _lib.dtype_code(logits.dtype),
+                                    tokens.data_ptr(), pos.data_ptr(), history.data_ptr(), history.stride(0),
+                                    steps.data_ptr(), history.shape[1], _lib.current_stream(logits.device))
+    _lib.check(rc, "greedy_advance")
+
+
 class Qwen3:
     """The model on one HIP device, attention through this package's containers."""
 
@@ -213,15 +259,16 @@ class Qwen3:
         return self.logits(x[0, packed.last_token_index])
 
     # ------------------------------------------------------------------ decode
-    def _decode_stack(self, x: torch.Tensor, attend) -> torch.Tensor:
+    def _decode_stack(self, x: torch.Tensor, attend, h0: torch.Tensor | None = None) -> torch.Tensor:
         """The 28 layers of a decode step on the ``(B, C)`` residual stream ``x`` (updated in
         place): residual adds fused with the next RMSNorm (``add_rms_norm``), one GEMM for
         q/k/v and one for gate/up, SiLU * up in one launch, and ``attend(i, qkv)`` giving
         layer i's attention output ``(B, H * D)`` from its packed projection. Returns the
-        final RMSNorm of the stream (the lm_head input). Same arithmetic as the reference's
-        block (``model/layers.py:365-367``) op by op."""
+        final RMSNorm of the stream (the lm_head input); ``h0``, when given, is layer 0's input
+        norm of ``x`` already computed. Same arithmetic as the reference's block
+        (``model/layers.py:365-367``) op by op."""
         c = self.cfg
-        _, h = add_rms_norm(x, None, self.w["l0.ln1"], c.eps)
+        h = h0 if h0 is not None else add_rms_norm(x, None, self.w["l0.ln1"], c.eps)[1]
         for i in range(c.n_layer):
             p = f"l{i}."
             y = attend(i, self._proj(h, self.w[p + "wqkv"]))
@@ -276,10 +323,11 @@ class GraphDecoder:
     """Greedy decode steps of a fixed batch, each replayed from one captured HIP graph.
 
     Device state per row: the next input token, its position, an int32 seqlen, and the
-    row's block table; every step computes the write slot ``table[pos // bs] * bs + pos % bs``
-    (reference ``model/paged.py:499-501``) and ``seqlen = pos + 1`` on the device, runs the
-    28 layers (HIP slot write + HIP paged decode per layer), takes the argmax and advances
-    ``pos``. ``history`` collects the generated tokens.
+    row's block table. A step is HIP launches only: one computes the write slot
+    ``table[pos // bs] * bs + pos % bs`` (reference ``model/paged.py:499-501``), ``seqlen =
+    pos + 1``, the embedding row and layer 0's input norm; then the 28 layers; then the
+    lm_head and one launch for the argmax, ``history``, the next tokens and ``pos + 1``.
+    ``history`` collects the generated tokens (``step_idx`` counts each row's steps).
     """
 
     def __init__(self, model: Qwen3, pool: PagedPool, tables: list[list[int]], lengths: list[int],
@@ -296,12 +344,13 @@ class GraphDecoder:
         for r, t in enumerate(tables):
             bt[r, : len(t)] = torch.tensor(t, dtype=torch.int32)
         self.table = bt.to(dev)
-        self.table64 = self.table.to(torch.int64)
         self.pos = torch.tensor(lengths, dtype=torch.long, device=dev)
         self.seqlen = (self.pos + 1).to(torch.int32)
         self.tokens = first_tokens.to(dev, torch.long).clone()
         self.history = torch.zeros(B, max_new, dtype=torch.long, device=dev)
-        self.step_idx = torch.zeros(1, dtype=torch.long, device=dev)
+        self.step_idx = torch.zeros(B, dtype=torch.long, device=dev)  # steps taken, per row
+        self.slots = torch.zeros(B, dtype=torch.long, device=dev)
+        self.error = torch.zeros(1, dtype=torch.int32, device=dev)
         self.max_new = max_new
         self.B = B
         q0 = torch.zeros(B, c.n_head, c.head_dim, dtype=model.dtype, device=dev)
@@ -311,9 +360,12 @@ class GraphDecoder:
 
     def _step(self) -> None:
         m, c, bs = self.model, self.model.cfg, self.pool.block_size
-        self.seqlen.copy_((self.pos + 1).to(torch.int32))
-        slots = self.table64.gather(1, (self.pos // bs).view(-1, 1)).view(-1) * bs + self.pos % bs
-        x = F.embedding(self.tokens, m.w["embed"])  # (B, C)
+        x = torch.empty(self.B, c.hidden, dtype=m.dtype, device=m.device)
+        h0 = torch.empty_like(x)
+        # seqlen, write slots, embedding lookup and layer 0's input norm: one launch
+        decode_step_begin(self.tokens, self.pos, self.table, bs, m.w["embed"], m.w["l0.ln1"], c.eps, self.seqlen,
+                          self.slots, x, h0, self.error)
+        slots = self.slots
 
         def attend(i: int, qkv) -> torch.Tensor:
             p = f"l{i}."
@@ -321,11 +373,9 @@ class GraphDecoder:
                                              self.pos, c.eps)
             return self.plan.run(i, q).view(self.B, -1)
 
-        nxt = argmax_rows(m._lm_head(m._decode_stack(x, attend)))
-        self.history.index_copy_(1, self.step_idx, nxt.view(-1, 1))
-        self.tokens.copy_(nxt)
-        self.pos.add_(1)
-        self.step_idx.add_(1)
+        # argmax, history, next tokens and positions: one launch
+        greedy_advance(m._lm_head(m._decode_stack(x, attend, h0)), self.tokens, self.pos, self.history,
+                       self.step_idx)
 
     def capture(self, stream=None) -> None:
         """Record one step (run once eagerly first so lazily built state exists) and undo

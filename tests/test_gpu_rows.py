@@ -18,7 +18,7 @@ import torch
 from miattn import PagedPool
 import torch.nn.functional as F
 
-from miattn.qwen3 import add_rms_norm, rope_table, silu_mul
+from miattn.qwen3 import add_rms_norm, decode_step_begin, greedy_advance, rms_norm, rope_table, silu_mul
 from miattn.rows import Parts, argmax_rows, glu_weight, rows_linear, rows_supported, rows_swiglu
 
 pytestmark = pytest.mark.gpu
@@ -187,4 +187,53 @@ def test_glu_weight_interleaves_by_16():
     w = glu_weight(wg, wu)
     assert torch.equal(w[0:16], wg[0:16]) and torch.equal(w[16:32], wu[0:16])
     assert torch.equal(w[32:48], wg[16:32]) and torch.equal(w[48:64], wu[16:32])
+
+
+def test_decode_step_begin_matches_the_tensor_ops():
+    g = torch.Generator().manual_seed(11)
+    B, C, V, bs, mb = 6, 1024, 1000, 16, 9
+    embed = torch.randn(V, C, generator=g).to(torch.bfloat16).cuda()
+    w = (1.0 + 0.1 * torch.randn(C, generator=g)).to(torch.bfloat16).cuda()
+    tokens = torch.randint(0, V, (B,), generator=g).cuda()
+    pos = torch.randint(0, mb * bs, (B,), generator=g).cuda()
+    table = torch.randperm(64, generator=g)[: B * mb].view(B, mb).to(torch.int32).cuda()
+    seqlen = torch.zeros(B, dtype=torch.int32, device="cuda")
+    slots = torch.zeros(B, dtype=torch.int64, device="cuda")
+    x = torch.empty(B, C, dtype=torch.bfloat16, device="cuda")
+    h = torch.empty_like(x)
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    decode_step_begin(tokens, pos, table, bs, embed, w, 1e-6, seqlen, slots, x, h, err)
+    torch.cuda.synchronize()
+    assert err.item() == 0
+    assert torch.equal(seqlen, (pos + 1).int())
+    assert torch.equal(slots, table.long().gather(1, (pos // bs).view(-1, 1)).view(-1) * bs + pos % bs)
+    assert torch.equal(x, embed[tokens])
+    want = rms_norm(embed[tokens], w, 1e-6)
+    assert (h == want).float().mean().item() > 0.999
+    # an out-of-range token or position is reported and its row left alone
+    tokens[2] = V
+    pos[4] = mb * bs
+    seqlen.zero_()
+    decode_step_begin(tokens, pos, table, bs, embed, w, 1e-6, seqlen, slots, x, h, err)
+    torch.cuda.synchronize()
+    assert err.item() in (3, 5) and seqlen[2].item() == 0 and seqlen[4].item() == 0 and seqlen[0].item() > 0
+
+
+def test_greedy_advance_updates_the_step_state():
+    g = torch.Generator().manual_seed(12)
+    B, V, max_new = 5, 3000, 3
+    logits = torch.randn(B, V, generator=g).to(torch.bfloat16).cuda()
+    tokens = torch.zeros(B, dtype=torch.int64, device="cuda")
+    pos = torch.arange(B, dtype=torch.int64, device="cuda") * 10
+    history = torch.full((B, max_new), -1, dtype=torch.int64, device="cuda")
+    steps = torch.tensor([0, 1, 2, 3, 0], dtype=torch.int64, device="cuda")  # row 3 is past its history
+    greedy_advance(logits, tokens, pos, history, steps)
+    torch.cuda.synchronize()
+    pick = logits.cpu().argmax(-1)
+    assert torch.equal(tokens.cpu(), pick)
+    assert torch.equal(pos.cpu(), torch.arange(B) * 10 + 1)
+    assert torch.equal(steps.cpu(), torch.tensor([1, 2, 3, 4, 1]))
+    h = history.cpu()
+    assert h[0, 0] == pick[0] and h[1, 1] == pick[1] and h[2, 2] == pick[2] and h[4, 0] == pick[4]
+    assert (h[3] == -1).all() and (h[0, 1:] == -1).all()
 
