@@ -141,6 +141,10 @@ int mi_decode_step_begin(const int64_t* tokens, const int64_t* pos, const int32_
                          int32_t* error_word, void* stream);
 int mi_greedy_advance(const void* logits, int64_t ld, int rows, int cols, int dtype, int64_t* tokens, int64_t* pos,
                       int64_t* history, int64_t hist_stride, int64_t* steps, int max_steps, void* stream);
+/* mi_greedy_advance from mi_rows_gemm_argmax's per-tile picks (rows x n_tiles) instead of the
+ * logits: the same pick, token, history, step and position updates. */
+int mi_greedy_advance_tiles(const void* tile_best, int n_tiles, int rows, int64_t* tokens, int64_t* pos,
+                            int64_t* history, int64_t hist_stride, int64_t* steps, int max_steps, void* stream);
 
 /* ------------------------------------------------------------------ decode-step projections
  * out = a w^T for 1 <= M <= 32 rows (nn.Linear without bias, the reference's projections at
@@ -162,6 +166,13 @@ int mi_rows_gemm(const void* a, int64_t lda, const void* w, int64_t ldw, void* o
  * K <= 1024 (unsplit), other requirements as mi_rows_gemm. */
 int mi_rows_gemm_glu(const void* a, int64_t lda, const void* w_glu, int64_t ldw, void* out, int64_t ldo,
                      int M, int inter, int K, int dtype, void* stream);
+/* An unsplit product (K % 256 == 0, K <= 1024) that also picks, for each row and each
+ * 32-column tile t, the tile's best column under torch.argmax's rule on the outputs rounded
+ * to `dtype` (largest value, lowest column on ties, NaN above every number):
+ * tile_best[row * n_tiles + t] = {float value, int32 column}, n_tiles = ceil(N / 32). out may be NULL (the
+ * products are then not stored). For a greedy step's lm_head with mi_greedy_advance_tiles. */
+int mi_rows_gemm_argmax(const void* a, int64_t lda, const void* w, int64_t ldw, void* out, int64_t ldo,
+                        void* tile_best, int M, int N, int K, int dtype, void* stream);
 
 /* ------------------------------------------------------------------ paged decode
  * Replaces paged_decode (reference model/triton_decode.py:250-328) and its kernel

@@ -251,6 +251,34 @@ struct Advance {
   int max_steps;
 };
 
+// Workgroup-wide reduction of the threads' (value, index) candidates, then thread 0 writes
+// the pick (out, and the step's advance when requested).
+__device__ __forceinline__ void finish_pick(Best b, Best* part, int row, int64_t* out, const Advance& adv) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(b.v, off, 64);
+    const int oi = __shfl_xor(b.i, off, 64);
+    if (better(ov, oi, b)) b = Best{ov, oi};
+  }
+  if ((tid & 63) == 0) part[tid >> 6] = b;
+  __syncthreads();
+  if (tid == 0) {
+    Best r = part[0];
+    for (int k = 1; k < int(blockDim.x) / 64; ++k) {
+      if (better(part[k].v, part[k].i, r)) r = part[k];
+    }
+    if (out != nullptr) out[row] = r.i;
+    if (adv.tokens != nullptr) {
+      adv.tokens[row] = r.i;
+      const int64_t st = adv.steps[row];
+      if (st >= 0 && st < adv.max_steps) adv.history[row * adv.hist_stride + st] = r.i;
+      adv.steps[row] = st + 1;
+      adv.pos[row] += 1;
+    }
+  }
+}
+
 // One workgroup per row; each thread walks 8-element (16-byte) pieces of the row 4 at a time
 // (all 4 loads in flight), then the workgroup reduces (value, index) pairs.
 template <typename T>
@@ -295,29 +323,22 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_rows_kernel(const T* __
       if (better(v, i, b)) b = Best{v, i};
     }
   }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const float ov = __shfl_xor(b.v, off, 64);
-    const int oi = __shfl_xor(b.i, off, 64);
-    if (better(ov, oi, b)) b = Best{ov, oi};
+  finish_pick(b, part, row, out, adv);
+}
+
+// Greedy pick from per-tile results (the lm_head launch's best (value, column) of each
+// 32-column tile for each row, row-major: tiles[row * n_tiles + t]): the same rule applied to
+// the tiles' winners gives the row's first maximum.
+__global__ __launch_bounds__(kArgmaxThreads) void pick_tiles_kernel(const Best* __restrict__ tiles, int n_tiles,
+                                                                    int rows, int64_t* __restrict__ out, Advance adv) {
+  __shared__ Best part[kArgmaxThreads / 64];
+  const int row = blockIdx.x;
+  Best b{-INFINITY, INT_MAX};
+  for (int t = threadIdx.x; t < n_tiles; t += kArgmaxThreads) {
+    const Best c = tiles[int64_t(row) * n_tiles + t];
+    if (better(c.v, c.i, b)) b = c;
   }
-  if ((tid & 63) == 0) part[tid >> 6] = b;
-  __syncthreads();
-  if (tid == 0) {
-    Best r = part[0];
-#pragma unroll
-    for (int k = 1; k < kArgmaxThreads / 64; ++k) {
-      if (better(part[k].v, part[k].i, r)) r = part[k];
-    }
-    if (out != nullptr) out[row] = r.i;
-    if (adv.tokens != nullptr) {
-      adv.tokens[row] = r.i;
-      const int64_t st = adv.steps[row];
-      if (st >= 0 && st < adv.max_steps) adv.history[row * adv.hist_stride + st] = r.i;
-      adv.steps[row] = st + 1;
-      adv.pos[row] += 1;
-    }
-  }
+  finish_pick(b, part, row, out, adv);
 }
 
 template <typename T>
@@ -455,4 +476,23 @@ extern "C" int mi_decode_step_begin(const int64_t* tokens, const int64_t* pos, c
                                             vocab, norm_w, cols, eps, seqlen, slots, x, h, B, error_word, s);
     default: return fail(MI_ERR_INVALID, "mi_decode_step_begin: unknown dtype %d", dtype);
   }
+}
+
+extern "C" int mi_greedy_advance_tiles(const void* tile_best, int n_tiles, int rows, int64_t* tokens, int64_t* pos,
+                                       int64_t* history, int64_t hist_stride, int64_t* steps, int max_steps,
+                                       void* stream) {
+  using namespace miattn;
+  if (rows < 0 || n_tiles < 1 || max_steps < 0 || hist_stride < max_steps) {
+    return fail(MI_ERR_INVALID, "mi_greedy_advance_tiles: bad shape rows=%d n_tiles=%d max_steps=%d", rows, n_tiles,
+                max_steps);
+  }
+  if (tile_best == nullptr || tokens == nullptr || pos == nullptr || steps == nullptr ||
+      (max_steps > 0 && history == nullptr)) {
+    return fail(MI_ERR_INVALID, "mi_greedy_advance_tiles: NULL pointer");
+  }
+  if (rows == 0) return MI_OK;
+  const Advance adv{tokens, pos, history, hist_stride, steps, max_steps};
+  hipLaunchKernelGGL(pick_tiles_kernel, dim3(rows), dim3(kArgmaxThreads), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const Best*>(tile_best), n_tiles, rows, nullptr, adv);
+  return launch_status("mi_greedy_advance_tiles");
 }

@@ -21,6 +21,8 @@
 //     written as T (S = 1) or as fp32 partials [S][M][N] that the consumer sums in split
 //     order and rounds once (the same single rounding nn.Linear's output gets).
 // Rows past M and columns past N read a clamped valid row and are never stored.
+#include <climits>
+
 #include "common.h"
 
 namespace miattn {
@@ -104,11 +106,22 @@ __device__ __forceinline__ float round_t(float x) {
 // out[i, 16t + c] = silu(g) * u with g, u the tile's columns c and 16 + c, rounded as the
 // reference's F.silu(gate(x)) * up(x) is: g and u to T, silu(g) = g / (1 + exp(-g)) in fp32 to
 // T, the product to T.
+// A tile's best column of each row under torch.argmax's rule on the rounded outputs: the
+// largest value, the lowest column on ties, NaN above every number.
+struct TileBest {
+  float v;
+  int i;
+};
+
+// best != null (unsplit launches only): each workgroup also writes, per row, its 32 columns'
+// best (value as rounded to T, column) to best[row * n_tiles + blockIdx.x], and writes the
+// outputs themselves only when out != null.
 template <typename T, int NIT, bool kGLU>
 __global__ __launch_bounds__(256) void rows_gemm_kernel(const T* __restrict__ a, int64_t lda,
                                                         const T* __restrict__ w, int64_t ldw,
                                                         T* __restrict__ out, int64_t ldo,
-                                                        float* __restrict__ part, int M, int N, int K) {
+                                                        float* __restrict__ part, int M, int N, int K,
+                                                        TileBest* __restrict__ best) {
   constexpr int kRegion = NIT * 256 * (stage_a<NIT>() ? 2 : 1);  // 16-byte slots per wave
   __shared__ uint4 lds[kGemmWaves * kRegion];
   const int tid = threadIdx.x;
@@ -179,6 +192,24 @@ __global__ __launch_bounds__(256) void rows_gemm_kernel(const T* __restrict__ a,
     const int r = e >> 6, ln = e & 63;
     const int i = 8 * (r >> 2) + 4 * (ln >> 5) + (r & 3);  // accumulator row (activation row)
     const int n = n0 + (ln & 31);                            // accumulator column
+    if (best != nullptr) {  // wave-uniform: the 32 lanes of each half hold one row's 32 columns
+      // first maximum of the half: the max over its non-NaN columns (DPP), then the lowest
+      // lane holding it; a NaN column, if any, wins instead (the lowest NaN lane)
+      const bool valid = n < N;
+      const float vr = to_f32(from_f32<T>(v));
+      const bool is_nan = valid && vr != vr;
+      const float vv = valid && !is_nan ? vr : -INFINITY;
+      const float mx = group_allreduce<32, MaxOp>(vv);
+      const int sh = (ln >> 5) * 32;
+      const uint32_t nan_lanes = uint32_t(__ballot(is_nan) >> sh);
+      const uint32_t max_lanes = uint32_t(__ballot(valid && !is_nan && vv == mx) >> sh);
+      if ((ln & 31) == 0 && i < M) {
+        const int jn = __builtin_ffs(int(nan_lanes)) - 1, jm = __builtin_ffs(int(max_lanes)) - 1;
+        best[int64_t(i) * gridDim.x + blockIdx.x] =
+            nan_lanes != 0 ? TileBest{__builtin_nanf(""), n0 + jn} : TileBest{mx, n0 + jm};
+      }
+      if (out == nullptr) continue;
+    }
     if (i < M && n < N) {
       if (part == nullptr) {
         out[int64_t(i) * ldo + n] = from_f32<T>(v);
@@ -191,16 +222,16 @@ __global__ __launch_bounds__(256) void rows_gemm_kernel(const T* __restrict__ a,
 
 template <typename T, bool kGLU>
 int launch_rows(const void* a, int64_t lda, const void* w, int64_t ldw, void* out, int64_t ldo, float* part,
-                int M, int N, int K, int S, int nit, hipStream_t s) {
+                int M, int N, int K, int S, int nit, hipStream_t s, TileBest* best = nullptr) {
   const dim3 grid((N + kTile - 1) / kTile, S), block(256);
   const T* at = static_cast<const T*>(a);
   const T* wt = static_cast<const T*>(w);
   T* ot = static_cast<T*>(out);
   switch (nit) {
-    case 1: hipLaunchKernelGGL((rows_gemm_kernel<T, 1, kGLU>), grid, block, 0, s, at, lda, wt, ldw, ot, ldo, part, M, N, K); break;
-    case 2: hipLaunchKernelGGL((rows_gemm_kernel<T, 2, kGLU>), grid, block, 0, s, at, lda, wt, ldw, ot, ldo, part, M, N, K); break;
-    case 3: hipLaunchKernelGGL((rows_gemm_kernel<T, 3, kGLU>), grid, block, 0, s, at, lda, wt, ldw, ot, ldo, part, M, N, K); break;
-    default: hipLaunchKernelGGL((rows_gemm_kernel<T, 4, kGLU>), grid, block, 0, s, at, lda, wt, ldw, ot, ldo, part, M, N, K); break;
+    case 1: hipLaunchKernelGGL((rows_gemm_kernel<T, 1, kGLU>), grid, block, 0, s, at, lda, wt, ldw, ot, ldo, part, M, N, K, best); break;
+    case 2: hipLaunchKernelGGL((rows_gemm_kernel<T, 2, kGLU>), grid, block, 0, s, at, lda, wt, ldw, ot, ldo, part, M, N, K, best); break;
+    case 3: hipLaunchKernelGGL((rows_gemm_kernel<T, 3, kGLU>), grid, block, 0, s, at, lda, wt, ldw, ot, ldo, part, M, N, K, best); break;
+    default: hipLaunchKernelGGL((rows_gemm_kernel<T, 4, kGLU>), grid, block, 0, s, at, lda, wt, ldw, ot, ldo, part, M, N, K, best); break;
   }
   return launch_status(kGLU ? "mi_rows_gemm_glu" : "mi_rows_gemm");
 }
@@ -289,5 +320,35 @@ extern "C" int mi_rows_gemm_glu(const void* a, int64_t lda, const void* w_glu, i
     case MI_BF16: return launch_rows<bf16_t, true>(a, lda, w_glu, ldw, out, ldo, nullptr, M, 2 * inter, K, 1, nit, s);
     case MI_F16: return launch_rows<f16_t, true>(a, lda, w_glu, ldw, out, ldo, nullptr, M, 2 * inter, K, 1, nit, s);
     default: return fail(MI_ERR_UNSUPPORTED, "mi_rows_gemm_glu: dtype %d (bf16 and fp16 only)", dtype);
+  }
+}
+
+extern "C" int mi_rows_gemm_argmax(const void* a, int64_t lda, const void* w, int64_t ldw, void* out, int64_t ldo,
+                                   void* tile_best, int M, int N, int K, int dtype, void* stream) {
+  using namespace miattn;
+  if (M < 1 || M > kTile || N < 1 || K < 1) {
+    return fail(MI_ERR_INVALID, "mi_rows_gemm_argmax: bad shape M=%d N=%d K=%d (1 <= M <= %d)", M, N, K, kTile);
+  }
+  if (K % (kGemmWaves * kStepK) != 0 || K / (kGemmWaves * kStepK) > 4) {
+    return fail(MI_ERR_UNSUPPORTED, "mi_rows_gemm_argmax: K=%d must be a multiple of %d and at most %d", K,
+                kGemmWaves * kStepK, 4 * kGemmWaves * kStepK);
+  }
+  if (a == nullptr || w == nullptr || tile_best == nullptr) {
+    return fail(MI_ERR_INVALID, "mi_rows_gemm_argmax: NULL pointer argument");
+  }
+  if (lda < K || ldw < K || (out != nullptr && ldo < N)) {
+    return fail(MI_ERR_INVALID, "mi_rows_gemm_argmax: row strides (%lld, %lld, %lld) shorter than the rows",
+                (long long)lda, (long long)ldw, (long long)ldo);
+  }
+  if ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(w)) % 16 != 0 || lda % 8 != 0 || ldw % 8 != 0) {
+    return fail(MI_ERR_UNSUPPORTED, "mi_rows_gemm_argmax: A and W need 16-byte aligned rows");
+  }
+  const int nit = K / (kGemmWaves * kStepK);
+  TileBest* best = static_cast<TileBest*>(tile_best);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case MI_BF16: return launch_rows<bf16_t, false>(a, lda, w, ldw, out, ldo, nullptr, M, N, K, 1, nit, s, best);
+    case MI_F16: return launch_rows<f16_t, false>(a, lda, w, ldw, out, ldo, nullptr, M, N, K, 1, nit, s, best);
+    default: return fail(MI_ERR_UNSUPPORTED, "mi_rows_gemm_argmax: dtype %d (bf16 and fp16 only)", dtype);
   }
 }

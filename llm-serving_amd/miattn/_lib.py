@@ -83,6 +83,15 @@ SIGNATURES: dict[str, tuple] = {
         [_c_void_p, _c_int64, _c_void_p, _c_int64, _c_void_p, _c_int64, _c_int, _c_int, _c_int, _c_int, _c_void_p],
     ),
     "mi_argmax_rows": (_c_int, [_c_void_p, _c_int64, _c_int, _c_int, _c_void_p, _c_int, _c_void_p]),
+    "mi_rows_gemm_argmax": (
+        _c_int,
+        [_c_void_p, _c_int64, _c_void_p, _c_int64, _c_void_p, _c_int64, _c_void_p, _c_int, _c_int, _c_int, _c_int,
+         _c_void_p],
+    ),
+    "mi_greedy_advance_tiles": (
+        _c_int,
+        [_c_void_p, _c_int, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_int64, _c_void_p, _c_int, _c_void_p],
+    ),
     "mi_decode_step_begin": (
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_int64, _c_int, _c_int, _c_void_p, _c_int64, _c_void_p, _c_int,

@@ -33,7 +33,7 @@ from . import _lib
 from .decode import paged_decode_plan
 from .packed import PackedPrefill
 from .paged import PagedKV, PagedPool, PagedWriteSink
-from .rows import Parts, argmax_rows, glu_weight, rows_linear, rows_supported, rows_swiglu
+from .rows import Parts, argmax_rows, glu_weight, rows_linear, rows_supported, rows_swiglu, rows_tile_best
 
 __all__ = ["Qwen3Config", "random_weights", "Qwen3", "GraphDecoder"]
 
@@ -173,6 +173,28 @@ def decode_step_begin(tokens: torch.Tensor, pos: torch.Tensor, table: torch.Tens
     _lib.check(rc, "decode_step_begin")
 
 
+def _check_step_state(B: int, tokens, pos, history, steps) -> None:
+    for name, t in (("tokens", tokens), ("pos", pos), ("steps", steps)):
+        if t.dtype != torch.int64 or t.numel() != B or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous int64 tensor of {B} rows")
+    if history.dtype != torch.int64 or history.dim() != 2 or history.shape[0] != B or history.stride(1) != 1:
+        raise ValueError(f"history must be an int64 ({B}, max_steps) tensor with contiguous rows")
+
+
+def greedy_advance_tiles(tiles: torch.Tensor, tokens: torch.Tensor, pos: torch.Tensor, history: torch.Tensor,
+                         steps: torch.Tensor) -> None:
+    """:func:`greedy_advance` from ``rows_tile_best``'s per-tile picks ``(B, n_tiles, 2)``
+    (``mi_greedy_advance_tiles``): the same pick and updates without the logits."""
+    if tiles.dtype != torch.int32 or tiles.dim() != 3 or tiles.shape[2] != 2 or not tiles.is_contiguous():
+        raise ValueError("tiles must be the contiguous (B, n_tiles, 2) int32 output of rows_tile_best")
+    B, n_tiles, _ = tiles.shape
+    _check_step_state(B, tokens, pos, history, steps)
+    rc = _lib.lib.mi_greedy_advance_tiles(tiles.data_ptr(), n_tiles, B, tokens.data_ptr(), pos.data_ptr(),
+                                          history.data_ptr(), history.stride(0), steps.data_ptr(), history.shape[1],
+                                          _lib.current_stream(tiles.device))
+    _lib.check(rc, "greedy_advance_tiles")
+
+
 def greedy_advance(logits: torch.Tensor, tokens: torch.Tensor, pos: torch.Tensor, history: torch.Tensor,
                    steps: torch.Tensor) -> None:
     """One HIP launch (``mi_greedy_advance``) for the end of a greedy decode step, in place:
@@ -181,11 +203,7 @@ def greedy_advance(logits: torch.Tensor, tokens: torch.Tensor, pos: torch.Tensor
     B, V = logits.shape
     if logits.stride(1) != 1:
         raise ValueError("logits must have unit element stride")
-    for name, t in (("tokens", tokens), ("pos", pos), ("steps", steps)):
-        if t.dtype != torch.int64 or t.numel() != B or not t.is_contiguous():
-            raise ValueError(f"{name} must be a contiguous int64 tensor of {B} rows")
-    if history.dtype != torch.int64 or history.dim() != 2 or history.shape[0] != B or history.stride(1) != 1:
-        raise ValueError(f"history must be an int64 ({B}, max_steps) tensor with contiguous rows")
+    _check_step_state(B, tokens, pos, history, steps)
     rc = _lib.lib.mi_greedy_advance(logits.data_ptr(), logits.stride(0), B, V, _lib.dtype_code(logits.dtype),
                                     tokens.data_ptr(), pos.data_ptr(), history.data_ptr(), history.stride(0),
                                     steps.data_ptr(), history.shape[1], _lib.current_stream(logits.device))
@@ -373,9 +391,14 @@ class GraphDecoder:
                                              self.pos, c.eps)
             return self.plan.run(i, q).view(self.B, -1)
 
-        # argmax, history, next tokens and positions: one launch
-        greedy_advance(m._lm_head(m._decode_stack(x, attend, h0)), self.tokens, self.pos, self.history,
-                       self.step_idx)
+        h = m._decode_stack(x, attend, h0)
+        w = m.w["embed"]
+        if rows_supported(h, w) and h.shape[1] <= 1024:
+            # lm_head reduced to per-tile picks in its own launch (the logits are not stored),
+            # then the pick, history, next tokens and positions in one more
+            greedy_advance_tiles(rows_tile_best(h, w), self.tokens, self.pos, self.history, self.step_idx)
+        else:
+            greedy_advance(m._lm_head(h), self.tokens, self.pos, self.history, self.step_idx)
 
     def capture(self, stream=None) -> None:
         """Record one step (run once eagerly first so lazily built state exists) and undo

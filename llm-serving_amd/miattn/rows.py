@@ -17,7 +17,8 @@ import torch
 
 from . import _lib
 
-__all__ = ["MAX_ROWS", "Parts", "argmax_rows", "glu_weight", "rows_linear", "rows_swiglu", "rows_supported", "split_for"]
+__all__ = ["MAX_ROWS", "Parts", "argmax_rows", "glu_weight", "rows_linear", "rows_swiglu", "rows_supported",
+           "rows_tile_best", "split_for"]
 
 MAX_ROWS = 32
 _K_UNIT = 256  # k per workgroup step: 4 waves x 64
@@ -133,6 +134,28 @@ def rows_swiglu(x: torch.Tensor, w_glu: torch.Tensor) -> torch.Tensor:
                                    inter, M, inter, K, _lib.dtype_code(x.dtype), _lib.current_stream(x.device))
     _lib.check(rc, "rows_swiglu")
     return out
+
+
+def rows_tile_best(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """The unsplit product ``x @ w.T`` (into ``out`` when given, else not stored) reduced, per
+    row and per 32-column tile, to the tile's best column under ``torch.argmax``'s rule on
+    the rounded outputs (``mi_rows_gemm_argmax``). Returns ``(M, n_tiles, 2)`` int32: word 0
+    the value's fp32 bits, word 1 the column -- the input of ``greedy_advance_tiles``."""
+    _lib.require_library("rows_tile_best")
+    if not rows_supported(x, w) or x.shape[1] > 4 * _K_UNIT:
+        raise ValueError(f"rows_tile_best needs an unsplit rows product (K <= {4 * _K_UNIT}), got x "
+                         f"{tuple(x.shape)} w {tuple(w.shape)}")
+    M, K = x.shape
+    N = int(w.shape[0])
+    if out is not None and (tuple(out.shape) != (M, N) or out.dtype != x.dtype or out.stride(1) != 1):
+        raise ValueError(f"out must be ({M}, {N}) {x.dtype} with unit element stride")
+    tiles = torch.empty((M, (N + 31) // 32, 2), dtype=torch.int32, device=x.device)
+    rc = _lib.lib.mi_rows_gemm_argmax(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0),
+                                      None if out is None else out.data_ptr(), 0 if out is None else out.stride(0),
+                                      tiles.data_ptr(), M, N, K, _lib.dtype_code(x.dtype),
+                                      _lib.current_stream(x.device))
+    _lib.check(rc, "rows_tile_best")
+    return tiles
 
 
 def argmax_rows(x: torch.Tensor) -> torch.Tensor:

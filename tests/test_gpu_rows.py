@@ -18,8 +18,9 @@ import torch
 from miattn import PagedPool
 import torch.nn.functional as F
 
-from miattn.qwen3 import add_rms_norm, decode_step_begin, greedy_advance, rms_norm, rope_table, silu_mul
-from miattn.rows import Parts, argmax_rows, glu_weight, rows_linear, rows_supported, rows_swiglu
+from miattn.qwen3 import (add_rms_norm, decode_step_begin, greedy_advance, greedy_advance_tiles, rms_norm,
+                          rope_table, silu_mul)
+from miattn.rows import Parts, argmax_rows, glu_weight, rows_linear, rows_supported, rows_swiglu, rows_tile_best
 
 pytestmark = pytest.mark.gpu
 
@@ -236,4 +237,59 @@ def test_greedy_advance_updates_the_step_state():
     h = history.cpu()
     assert h[0, 0] == pick[0] and h[1, 1] == pick[1] and h[2, 2] == pick[2] and h[4, 0] == pick[4]
     assert (h[3] == -1).all() and (h[0, 1:] == -1).all()
+
+
+@pytest.mark.parametrize("M,N,K", [(32, 151936, 1024), (5, 1000, 512), (3, 70, 256)])
+def test_lm_head_tile_picks_give_the_argmax_of_the_logits(M, N, K):
+    g = torch.Generator().manual_seed(M + N)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16).cuda()
+    w = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16).cuda()
+    w[N // 2] = w[N // 3]  # identical weight rows: equal logits in two tiles, the lower column wins
+    x[0] = w[N // 3].float().sign().to(torch.bfloat16)  # row 0's maximum is at that tie
+    logits = rows_linear(x, w, n_split=1)
+    out = torch.empty_like(logits)
+    tiles = rows_tile_best(x, w, out)
+    assert torch.equal(out, logits)  # the same products, stored when asked
+    tiles_nolog = rows_tile_best(x, w)
+    assert torch.equal(tiles, tiles_nolog)
+    B = M
+    tokens = torch.zeros(B, dtype=torch.int64, device="cuda")
+    pos = torch.zeros(B, dtype=torch.int64, device="cuda")
+    history = torch.zeros(B, 2, dtype=torch.int64, device="cuda")
+    steps = torch.zeros(B, dtype=torch.int64, device="cuda")
+    greedy_advance_tiles(tiles, tokens, pos, history, steps)
+    torch.cuda.synchronize()
+    want = logits.cpu().argmax(-1)
+    assert torch.equal(tokens.cpu(), want) and torch.equal(history[:, 0].cpu(), want)
+    # each tile's pick is its own first maximum
+    t = tiles.cpu()
+    vals = t[..., 0].view(torch.float32)
+    lg = logits.float().cpu()
+    for tile in (0, (N - 1) // 32):
+        seg = lg[:, tile * 32:(tile + 1) * 32]
+        assert torch.equal(t[:, tile, 1].long(), seg.argmax(-1) + tile * 32)
+        assert torch.equal(vals[:, tile], seg.max(-1).values)
+
+
+def test_tile_picks_follow_torch_on_ties_and_nan():
+    # a weight matrix whose products hold exact ties and a NaN: x = e_0, so logits row r
+    # are column 0 of w (rows of w scaled per output column)
+    K, N = 256, 96
+    w = torch.zeros(N, K)
+    w[:, 0] = torch.tensor([float(c % 5) for c in range(N)])  # max 4.0 first at column 4, repeats
+    w[70, 0] = 4.0
+    x = torch.zeros(3, K)
+    x[:, 0] = 1.0
+    x[2, 0] = -1.0  # row 2: max 0.0 first at column 0
+    wb, xb = w.to(torch.bfloat16).cuda(), x.to(torch.bfloat16).cuda()
+    wn = wb.clone()
+    wn[40, 0] = float("nan")  # a NaN product in tile 1 beats every number
+    for weight, want in ((wb, [4, 4, 0]), (wn, [40, 40, 40])):
+        tiles = rows_tile_best(xb, weight)
+        tokens = torch.zeros(3, dtype=torch.int64, device="cuda")
+        greedy_advance_tiles(tiles, tokens, torch.zeros_like(tokens), torch.zeros(3, 1, dtype=torch.int64,
+                             device="cuda"), torch.zeros_like(tokens))
+        torch.cuda.synchronize()
+        assert tokens.cpu().tolist() == want
+        assert torch.equal(tokens.cpu(), (xb.float() @ weight.float().t()).to(torch.bfloat16).cpu().argmax(-1))
 
