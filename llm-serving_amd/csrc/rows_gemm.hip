@@ -8,9 +8,9 @@
 // weight matrix in flight at once across the chip. Layout:
 //   * grid (ceil(N / 32), S): a workgroup owns 32 output columns and 1/S of K; its 4 waves
 //     split that K range again, each wave KW = K / (4 S) contiguous k (NIT x 64);
-//   * every load a wave makes is issued before its first MFMA. W (and A, when it fits) is
-//     loaded in whole 128-byte lines, 8 lanes per line, and turned into the MFMA operand
-//     layout through the wave's own LDS region. Loading the operand layout directly (each
+//   * every load a wave makes is issued before its first MFMA. W and A are loaded in whole
+//     128-byte lines, 8 lanes per line, and turned into the MFMA operand layout through the
+//     wave's own LDS region, one 64-k step at a time. Loading the operand layout directly (each
 //     lane 16 bytes of its own row, 32 lines per instruction) measured 1.3-1.5x slower at
 //     the Qwen3-0.6B shapes, and 1.6x with the nontemporal hint (each line then fetched
 //     from L2 once per 16-byte piece);
@@ -63,9 +63,12 @@ __device__ __forceinline__ void stage_rows(const T* __restrict__ base, int64_t l
     }
   }
 }
-// Through the wave's LDS region into the MFMA operand layout (lane: row lane & 31, k-half
-// lane >> 5). 16-byte slots are XOR-swizzled by row: the writes and the operand reads are
-// both conflict-free.
+// Through the wave's LDS region (one 64-k step, 32 rows x 128 B) into the MFMA operand
+// layout (lane: row lane & 31, k-half lane >> 5), one step at a time through the same
+// region: every load is already in flight, so the region only has to hold the step being
+// converted, and the small region lets registers rather than LDS set the occupancy (the
+// lm_head launch: 77.5 -> 63.5 us against staging all steps at once). 16-byte slots are
+// XOR-swizzled by row: the writes and the operand reads are both conflict-free.
 template <int NIT>
 __device__ __forceinline__ void to_operands(uint4* __restrict__ lds, uint4 (&frag)[NIT][4]) {
   const int lane = threadIdx.x & 63;
@@ -76,22 +79,14 @@ __device__ __forceinline__ void to_operands(uint4* __restrict__ lds, uint4 (&fra
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int row = q * 8 + rr;
-      lds[it * 256 + row * 8 + (cc ^ (row & 7))] = frag[it][q];
+      lds[row * 8 + (cc ^ (row & 7))] = frag[it][q];
     }
-  }
-  __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_wave_barrier();
 #pragma unroll
-  for (int it = 0; it < NIT; ++it) {
-#pragma unroll
-    for (int s = 0; s < 4; ++s) frag[it][s] = lds[it * 256 + j * 8 + ((hf * 4 + s) ^ (j & 7))];
+    for (int s = 0; s < 4; ++s) frag[it][s] = lds[j * 8 + ((hf * 4 + s) ^ (j & 7))];
+    __builtin_amdgcn_wave_barrier();
   }
 }
-
-// A is staged like W when its region fits beside W's (NIT <= 2: 64 KiB per workgroup in
-// all); at NIT 3-4 the A operand is read straight into the operand layout (it is L2
-// resident: every workgroup reads the same rows).
-template <int NIT>
-constexpr bool stage_a() { return NIT <= 2; }
 
 // Round an fp32 result to T behind an empty asm, so the compiler cannot fold the op and the
 // rounding into a native fp16 op of different rounding.
@@ -122,13 +117,11 @@ __global__ __launch_bounds__(256) void rows_gemm_kernel(const T* __restrict__ a,
                                                         T* __restrict__ out, int64_t ldo,
                                                         float* __restrict__ part, int M, int N, int K,
                                                         TileBest* __restrict__ best) {
-  constexpr int kRegion = NIT * 256 * (stage_a<NIT>() ? 2 : 1);  // 16-byte slots per wave
+  constexpr int kRegion = 2 * 256;  // 16-byte slots per wave: one step of W, one of A
   __shared__ uint4 lds[kGemmWaves * kRegion];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int j = lane & 31;
-  const int hf = lane >> 5;
   const int n0 = blockIdx.x * kTile;
   const int split = blockIdx.y;
   constexpr int kw = NIT * kStepK;
@@ -137,19 +130,10 @@ __global__ __launch_bounds__(256) void rows_gemm_kernel(const T* __restrict__ a,
 
   uint4 wr[NIT][4], ar[NIT][4];
   stage_rows<T, NIT, true>(w + int64_t(n0) * ldw, ldw, N - 1 - n0, kb, wr);
-  if constexpr (stage_a<NIT>()) {
-    stage_rows<T, NIT, false>(a, lda, M - 1, kb, ar);
-  } else {
-    const char* ap = reinterpret_cast<const char*>(a + int64_t(min(j, M - 1)) * lda + kb + hf * 32);
-#pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-#pragma unroll
-      for (int s = 0; s < 4; ++s) ar[it][s] = load16(ap + (it * kStepK + s * 8) * int(sizeof(T)));
-    }
-  }
+  stage_rows<T, NIT, false>(a, lda, M - 1, kb, ar);
   __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the first use
   to_operands<NIT>(wl, wr);
-  if constexpr (stage_a<NIT>()) to_operands<NIT>(wl + NIT * 256, ar);
+  to_operands<NIT>(wl + 256, ar);
 
   floatx16 acc;
 #pragma unroll
