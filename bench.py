@@ -218,9 +218,11 @@ def bench_tpot(stream, prompt_len: int = 1920, new_tokens: int = 128, B: int = 3
     """Config 5 shape, closed batch: random-init Qwen3-0.6B, B rows of ``prompt_len`` random
     tokens prefilled in one packed group, then ``new_tokens`` greedy decode steps (context
     ``prompt_len`` -> ``prompt_len + new_tokens``). TPOT = GPU time of one whole decode step
-    (28 layers: projections, the HIP q/k-norm + RoPE + K/V write epilogue, HIP paged decode,
-    HIP residual add + RMSNorm and SiLU * up, the MLP GEMMs, lm_head,
-    argmax), replayed from one HIP graph; the eager (Python-launched) step is reported too."""
+    (step start: slots, seqlen, embedding, layer-0 norm; 28 layers: rows-GEMM projections, the
+    q/k-norm + RoPE + K/V write epilogue, paged decode + merge, residual add + RMSNorm,
+    gate/up + SiLU * up; lm_head with per-tile greedy picks; the pick and position advance --
+    all HIP launches), replayed from one HIP graph; the eager (Python-launched) step is
+    reported too."""
     from miattn import PagedKV
     from miattn.qwen3 import GraphDecoder, Qwen3, Qwen3Config, random_weights
 
