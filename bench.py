@@ -238,6 +238,11 @@ def bench_tpot(stream, prompt_len: int = 1920, new_tokens: int = 128, B: int = 3
     pool = model.new_pool(n_blocks, bs)
     with torch.cuda.stream(stream):
         torch.cuda.synchronize()
+        # the first prefill pays one-time costs (GEMM algorithm selection, the prefill
+        # schedule, allocator growth); the second, into the same slots, is the TTFT figure
+        with EventTimer(stream) as t:
+            model.prefill(prompts, pool, tables)
+        prefill_cold_ms = t.ms()
         with EventTimer(stream) as t:
             logits = model.prefill(prompts, pool, tables)
         prefill_ms = t.ms()
@@ -282,6 +287,7 @@ def bench_tpot(stream, prompt_len: int = 1920, new_tokens: int = 128, B: int = 3
         "decode_tokens_per_s": B * new_tokens / (total_ms * 1e-3),
         "eager_step_ms": eager_ms,
         "prefill_ms": prefill_ms,
+        "prefill_cold_ms": prefill_cold_ms,
         "prefill_tokens": B * prompt_len,
     }
 

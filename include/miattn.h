@@ -93,12 +93,16 @@ int mi_kv_slot_write(const void* k, const void* v, const void* slot_ids, int slo
  * [0, n_pos) or whose slot is outside [0, n_slots) is not written and 1 + its index goes to
  * *error_word (may be NULL). D = 64, 128 or 256. qkv_parts = 0: qkv holds `dtype` values;
  * qkv_parts = n >= 1: qkv holds fp32 split-K partial sums [n][B][row_stride] (mi_rows_gemm
- * with n_split = n), summed in split order and rounded once to `dtype` before the above. */
+ * with n_split = n), summed in split order and rounded once to `dtype` before the above.
+ * k_out / v_out (may be NULL): the roped k and the v rows also written packed, (B, H_kv, D)
+ * contiguous -- a packed prefill group's q/k norm + RoPE + slot write in one launch, its
+ * attention then reading q_out, k_out, v_out (reference model/packed.py:187-218). */
 int mi_qk_norm_rope_write(const void* qkv, int64_t row_stride, int qkv_parts, const void* q_norm_w,
                           const void* k_norm_w, const void* cos_tab, const void* sin_tab,
                           int64_t n_pos, const int64_t* pos, const void* slot_ids, int slot_bits,
-                          void* q_out, void* k_pool, void* v_pool, int B, int H, int H_kv, int D,
-                          int64_t n_slots, float eps, int dtype, int32_t* error_word, void* stream);
+                          void* q_out, void* k_pool, void* v_pool, void* k_out, void* v_out, int B, int H,
+                          int H_kv, int D, int64_t n_slots, float eps, int dtype, int32_t* error_word,
+                          void* stream);
 
 /* ------------------------------------------------------------------ decode-step small ops
  * The residual stream's add + RMSNorm and the MLP's SiLU(gate) * up, each one launch (the

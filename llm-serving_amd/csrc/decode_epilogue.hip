@@ -16,6 +16,9 @@
 // result equals the tensor-op chain's except where the fp32 sum's order moves a rounding
 // boundary.
 //
+// With k_out / v_out the roped k and the v of each row are also written packed, (B, H_kv, D)
+// contiguous, for a packed prefill's attention (the decode reads them from the pool).
+//
 // Layout: one wave per (row, head) over q, k and v heads of a packed projection row
 // [q (H x D) | k (H_kv x D) | v (H_kv x D)]; lane l holds the rotation pairs (p, p + D/2)
 // for p = l, l + 64, ... < D/2, so the pair partner is in the same lane. The projection
@@ -44,13 +47,13 @@ __global__ __launch_bounds__(256) void qk_norm_rope_write_kernel(
     const T* __restrict__ k_w,
     const T* __restrict__ cos_tab, const T* __restrict__ sin_tab, int64_t n_pos,
     const int64_t* __restrict__ pos, const IdxT* __restrict__ slots, T* __restrict__ q_out,
-    T* __restrict__ k_pool, T* __restrict__ v_pool, int B, int H, int H_kv, int64_t n_slots,
-    float eps, int32_t* __restrict__ err) {
+    T* __restrict__ k_pool, T* __restrict__ v_pool, T* __restrict__ k_out, T* __restrict__ v_out, int B, int H,
+    int H_kv, int64_t n_slots, float eps, int32_t* __restrict__ err) {
   constexpr int HALF = D / 2;
   constexpr int PPL = (HALF + 63) / 64;  // rotation pairs per lane
   const int lane = threadIdx.x & 63;
-  const int head = blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);  // over q, k, v heads
-  const int b = blockIdx.y;
+  const int head = blockIdx.y * (blockDim.x / 64) + (threadIdx.x >> 6);  // over q, k, v heads
+  const int b = blockIdx.x;
   const int n_heads = H + 2 * H_kv;
   if (head >= n_heads || b >= B) return;  // wave-uniform
   // a row whose position is outside the RoPE table or whose slot is outside the pool is
@@ -105,13 +108,19 @@ __global__ __launch_bounds__(256) void qk_norm_rope_write_kernel(
   }
 
   if (head >= H + H_kv) {  // v head: copied as is (exact: x1/x2 hold T values)
-    T* dst = v_pool + (int64_t(slot) * H_kv + (head - H - H_kv)) * D;
+    const int vh = head - H - H_kv;
+    T* dst = v_pool + (int64_t(slot) * H_kv + vh) * D;
+    T* dst2 = v_out != nullptr ? v_out + (int64_t(b) * H_kv + vh) * D : nullptr;
 #pragma unroll
     for (int j = 0; j < PPL; ++j) {
       const int p = lane + 64 * j;
       if (p < HALF) {
         dst[p] = from_f32<T>(x1[j]);
         dst[p + HALF] = from_f32<T>(x2[j]);
+        if (dst2 != nullptr) {
+          dst2[p] = from_f32<T>(x1[j]);
+          dst2[p + HALF] = from_f32<T>(x2[j]);
+        }
       }
     }
     return;
@@ -138,10 +147,12 @@ __global__ __launch_bounds__(256) void qk_norm_rope_write_kernel(
   }
 
   T* dst;
+  T* dst2 = nullptr;  // the packed k copy, when asked for
   if (is_q) {
     dst = q_out + (int64_t(b) * H + head) * D;
   } else {
     dst = k_pool + (int64_t(slot) * H_kv + (head - H)) * D;
+    if (k_out != nullptr) dst2 = k_out + (int64_t(b) * H_kv + (head - H)) * D;
   }
 #pragma unroll
   for (int j = 0; j < PPL; ++j) {
@@ -149,6 +160,10 @@ __global__ __launch_bounds__(256) void qk_norm_rope_write_kernel(
     if (p < HALF) {
       dst[p] = from_f32<T>(o1[j]);
       dst[p + HALF] = from_f32<T>(o2[j]);
+      if (dst2 != nullptr) {
+        dst2[p] = from_f32<T>(o1[j]);
+        dst2[p + HALF] = from_f32<T>(o2[j]);
+      }
     }
   }
 }
@@ -156,10 +171,10 @@ __global__ __launch_bounds__(256) void qk_norm_rope_write_kernel(
 template <typename T, int D>
 int launch_d(const void* qkv, int64_t row_stride, int parts, const void* q_w, const void* k_w, const void* cos_tab,
              const void* sin_tab, int64_t n_pos, const int64_t* pos, const void* slots, int slot_bits,
-             void* q_out, void* k_pool, void* v_pool, int B, int H, int H_kv, int64_t n_slots, float eps,
-             int32_t* err, hipStream_t s) {
+             void* q_out, void* k_pool, void* v_pool, void* k_out, void* v_out, int B, int H, int H_kv,
+             int64_t n_slots, float eps, int32_t* err, hipStream_t s) {
   constexpr int kWaves = 4;
-  const dim3 grid((H + 2 * H_kv + kWaves - 1) / kWaves, B);
+  const dim3 grid(B, (H + 2 * H_kv + kWaves - 1) / kWaves);
   const int64_t plane = int64_t(B) * row_stride;
   auto go = [&](auto idx_tag, auto unroll) {
     using IdxT = decltype(idx_tag);
@@ -167,7 +182,8 @@ int launch_d(const void* qkv, int64_t row_stride, int parts, const void* q_w, co
                        row_stride, parts, plane, static_cast<const T*>(q_w), static_cast<const T*>(k_w),
                        static_cast<const T*>(cos_tab), static_cast<const T*>(sin_tab), n_pos, pos,
                        static_cast<const IdxT*>(slots), static_cast<T*>(q_out), static_cast<T*>(k_pool),
-                       static_cast<T*>(v_pool), B, H, H_kv, n_slots, eps, err);
+                       static_cast<T*>(v_pool), static_cast<T*>(k_out), static_cast<T*>(v_out), B, H, H_kv,
+                       n_slots, eps, err);
   };
   auto by_slots = [&](auto unroll) {
     if (slot_bits == 32) go(int32_t{}, unroll); else go(int64_t{}, unroll);
@@ -184,15 +200,15 @@ int launch_d(const void* qkv, int64_t row_stride, int parts, const void* q_w, co
 template <typename T>
 int launch_t(int D, const void* qkv, int64_t row_stride, int parts, const void* q_w, const void* k_w, const void* cos_tab,
              const void* sin_tab, int64_t n_pos, const int64_t* pos, const void* slots, int slot_bits,
-             void* q_out, void* k_pool, void* v_pool, int B, int H, int H_kv, int64_t n_slots, float eps,
-             int32_t* err, hipStream_t s) {
+             void* q_out, void* k_pool, void* v_pool, void* k_out, void* v_out, int B, int H, int H_kv,
+             int64_t n_slots, float eps, int32_t* err, hipStream_t s) {
   switch (D) {
     case 64: return launch_d<T, 64>(qkv, row_stride, parts, q_w, k_w, cos_tab, sin_tab, n_pos, pos, slots, slot_bits,
-                                    q_out, k_pool, v_pool, B, H, H_kv, n_slots, eps, err, s);
+                                    q_out, k_pool, v_pool, k_out, v_out, B, H, H_kv, n_slots, eps, err, s);
     case 128: return launch_d<T, 128>(qkv, row_stride, parts, q_w, k_w, cos_tab, sin_tab, n_pos, pos, slots, slot_bits,
-                                      q_out, k_pool, v_pool, B, H, H_kv, n_slots, eps, err, s);
+                                      q_out, k_pool, v_pool, k_out, v_out, B, H, H_kv, n_slots, eps, err, s);
     case 256: return launch_d<T, 256>(qkv, row_stride, parts, q_w, k_w, cos_tab, sin_tab, n_pos, pos, slots, slot_bits,
-                                      q_out, k_pool, v_pool, B, H, H_kv, n_slots, eps, err, s);
+                                      q_out, k_pool, v_pool, k_out, v_out, B, H, H_kv, n_slots, eps, err, s);
     default:
       return fail(MI_ERR_UNSUPPORTED, "mi_qk_norm_rope_write: head_dim %d is not supported (64, 128, 256)", D);
   }
@@ -204,8 +220,9 @@ int launch_t(int D, const void* qkv, int64_t row_stride, int parts, const void* 
 extern "C" int mi_qk_norm_rope_write(const void* qkv, int64_t row_stride, int qkv_parts, const void* q_norm_w,
                                      const void* k_norm_w, const void* cos_tab, const void* sin_tab,
                                      int64_t n_pos, const int64_t* pos, const void* slot_ids, int slot_bits,
-                                     void* q_out, void* k_pool, void* v_pool, int B, int H, int H_kv, int D,
-                                     int64_t n_slots, float eps, int dtype, int32_t* error_word, void* stream) {
+                                     void* q_out, void* k_pool, void* v_pool, void* k_out, void* v_out, int B,
+                                     int H, int H_kv, int D, int64_t n_slots, float eps, int dtype,
+                                     int32_t* error_word, void* stream) {
   using namespace miattn;
   if (B < 0 || H < 1 || H_kv < 1 || H % H_kv != 0) {
     return fail(MI_ERR_INVALID, "mi_qk_norm_rope_write: n_head (%d) must be a multiple of n_kv_head (%d)", H, H_kv);
@@ -224,17 +241,16 @@ extern "C" int mi_qk_norm_rope_write(const void* qkv, int64_t row_stride, int qk
     return fail(MI_ERR_INVALID, "mi_qk_norm_rope_write: NULL pointer argument");
   }
   if (B == 0) return MI_OK;
-  if (B > 65535) return fail(MI_ERR_UNSUPPORTED, "mi_qk_norm_rope_write: at most 65535 rows, got %d", B);
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
     case MI_BF16: return launch_t<bf16_t>(D, qkv, row_stride, qkv_parts, q_norm_w, k_norm_w, cos_tab, sin_tab, n_pos, pos,
-                                          slot_ids, slot_bits, q_out, k_pool, v_pool, B, H, H_kv, n_slots, eps,
+                                          slot_ids, slot_bits, q_out, k_pool, v_pool, k_out, v_out, B, H, H_kv, n_slots, eps,
                                           error_word, s);
     case MI_F16: return launch_t<f16_t>(D, qkv, row_stride, qkv_parts, q_norm_w, k_norm_w, cos_tab, sin_tab, n_pos, pos,
-                                        slot_ids, slot_bits, q_out, k_pool, v_pool, B, H, H_kv, n_slots, eps,
+                                        slot_ids, slot_bits, q_out, k_pool, v_pool, k_out, v_out, B, H, H_kv, n_slots, eps,
                                         error_word, s);
     case MI_F32: return launch_t<float>(D, qkv, row_stride, qkv_parts, q_norm_w, k_norm_w, cos_tab, sin_tab, n_pos, pos,
-                                        slot_ids, slot_bits, q_out, k_pool, v_pool, B, H, H_kv, n_slots, eps,
+                                        slot_ids, slot_bits, q_out, k_pool, v_pool, k_out, v_out, B, H, H_kv, n_slots, eps,
                                         error_word, s);
     default:
       return fail(MI_ERR_INVALID, "mi_qk_norm_rope_write: unknown dtype %d", dtype);

@@ -157,6 +157,34 @@ class PackedPrefill:
             sink.set_kv(layer, (layer_k, layer_v))
             start = end
 
+    def write_rope(self, layer: int, qkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: torch.Tensor,
+                   cos: torch.Tensor, sin: torch.Tensor, eps: float):
+        """This layer's q/k RMSNorm + RoPE (at each token's request-local position) and the
+        group's K/V write in one HIP launch (``PagedPool.write_qk_norm_rope`` over the packed
+        projection ``qkv`` ``(total, (H + 2 H_kv) D)``), in place of the reference's tensor
+        ops and :meth:`write`. Needs one paged pool behind every sink. Returns packed
+        ``(1, total, H, D)`` q and ``(1, total, H_kv, D)`` k and v for :meth:`attend`."""
+        if self._packed_slots is None:
+            raise RuntimeError("write_rope needs every sink on one paged pool (use write() otherwise)")
+        pool, slots = self._packed_slots
+        for sink in self.sinks:
+            written = getattr(sink, "_written", None)
+            if written is not None and written[layer]:
+                raise RuntimeError(
+                    f"layer {layer} was already written: the paged write-through sink holds exactly one "
+                    "full prefill (past_len == 0)"
+                )
+        T = self.total_tokens
+        k = torch.empty((T, pool.n_kv_head, pool.head_dim), dtype=pool.dtype, device=qkv.device)
+        v = torch.empty_like(k)
+        q = pool.write_qk_norm_rope(layer, slots, qkv, q_norm_w, k_norm_w, cos, sin, self.positions, eps,
+                                    k_out=k, v_out=v)
+        for sink in self.sinks:
+            written = getattr(sink, "_written", None)
+            if written is not None:
+                written[layer] = True
+        return q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0)
+
     def attend(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
         """Per-request causal attention over the packed axis (reference ``:204-218``)."""
         if q.dim() != 4 or q.shape[0] != 1 or q.shape[1] != self.total_tokens:

@@ -175,7 +175,8 @@ class PagedPool:
 
     def write_qk_norm_rope(self, layer: int, slot_ids: torch.Tensor, qkv,
                            q_norm_w: torch.Tensor, k_norm_w: torch.Tensor, cos: torch.Tensor,
-                           sin: torch.Tensor, pos: torch.Tensor, eps: float) -> torch.Tensor:
+                           sin: torch.Tensor, pos: torch.Tensor, eps: float, *, k_out: torch.Tensor | None = None,
+                           v_out: torch.Tensor | None = None) -> torch.Tensor:
         """One decode step's attention epilogue in one HIP launch: per-head RMSNorm of q and k
         (weights ``q_norm_w``/``k_norm_w``, ``(head_dim,)``), NeoX RoPE at ``pos`` (int64,
         one per row) from the ``(n_pos, head_dim/2)`` ``cos``/``sin`` tables, k and v written
@@ -188,6 +189,8 @@ class PagedPool:
         ``PagedKV.write`` (``model/paged.py:503-520``); the kernel rounds each step to the
         pool dtype as those ops do. A row whose position is outside the tables or whose slot
         is outside the pool is not written and is reported by :meth:`check_writes`.
+        ``k_out``/``v_out`` (contiguous ``(B, n_kv_head, head_dim)``, optional) also receive the
+        roped k and the v rows packed -- a packed prefill group's attention inputs.
         """
         layer = self._check_layer(layer)
         H, H_kv, D = self.n_head, self.n_kv_head, self.head_dim
@@ -221,6 +224,10 @@ class PagedPool:
         tensors = (qkv_data, q_norm_w, k_norm_w, cos, sin, pos, slot_ids)
         if self.device.type != "cuda" or not all(t.is_cuda for t in tensors):
             raise RuntimeError("PagedPool.write_qk_norm_rope is a HIP kernel and needs CUDA (HIP) tensors")
+        for name, t in (("k_out", k_out), ("v_out", v_out)):
+            if t is not None and (tuple(t.shape) != (B, H_kv, D) or t.dtype != self.dtype or not t.is_contiguous()
+                                  or not t.is_cuda):
+                raise ValueError(f"{name} must be a contiguous ({B}, {H_kv}, {D}) {self.dtype} HIP tensor")
         slot_ids = slot_ids.contiguous()
         pos = pos.contiguous()
         q = torch.empty((B, H, D), dtype=self.dtype, device=self.device)
@@ -228,7 +235,8 @@ class PagedPool:
             qkv_ptr, qkv_row, qkv_parts, q_norm_w.data_ptr(), k_norm_w.data_ptr(), cos.data_ptr(),
             sin.data_ptr(), cos.shape[0], pos.data_ptr(), slot_ids.data_ptr(),
             32 if slot_ids.dtype == torch.int32 else 64, q.data_ptr(), self.keys[layer].data_ptr(),
-            self.values[layer].data_ptr(), B, H, H_kv, D, self.n_slots, float(eps),
+            self.values[layer].data_ptr(), None if k_out is None else k_out.data_ptr(),
+            None if v_out is None else v_out.data_ptr(), B, H, H_kv, D, self.n_slots, float(eps),
             _lib.dtype_code(self.dtype), self._write_error.data_ptr(), _lib.current_stream(qkv.device),
         )
         _lib.check(rc, "PagedPool.write_qk_norm_rope")

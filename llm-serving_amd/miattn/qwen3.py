@@ -230,21 +230,6 @@ class Qwen3:
         self.cos, self.sin = rope_table(cfg.head_dim, cfg.rope_theta, max_pos, self.device, self.dtype)
 
     # ------------------------------------------------------------------ pieces
-    def _qkv(self, i: int, x: torch.Tensor):
-        c, p = self.cfg, f"l{i}."
-        lead = x.shape[:-1]
-        q = rms_norm(F.linear(x, self.w[p + "wq"]).view(*lead, c.n_head, c.head_dim), self.w[p + "qn"], c.eps)
-        k = rms_norm(F.linear(x, self.w[p + "wk"]).view(*lead, c.n_kv_head, c.head_dim), self.w[p + "kn"], c.eps)
-        v = F.linear(x, self.w[p + "wv"]).view(*lead, c.n_kv_head, c.head_dim)
-        return q, k, v
-
-    def _mlp(self, i: int, x: torch.Tensor) -> torch.Tensor:
-        p = f"l{i}."
-        return F.linear(F.silu(F.linear(x, self.w[p + "wg"])) * F.linear(x, self.w[p + "wu"]), self.w[p + "wd"])
-
-    def logits(self, x: torch.Tensor) -> torch.Tensor:
-        return F.linear(rms_norm(x, self.w["norm"], self.cfg.eps), self.w["embed"])
-
     def new_pool(self, n_blocks: int, block_size: int = 16) -> PagedPool:
         c = self.cfg
         return PagedPool(c.n_layer, n_blocks, block_size, c.n_kv_head, c.head_dim, dtype=self.dtype,
@@ -254,7 +239,10 @@ class Qwen3:
     def prefill(self, prompts: list[list[int]], pool: PagedPool, tables: list[list[int]]) -> torch.Tensor:
         """Packed prefill of whole prompts (reference ``MiniLLM.forward`` packed branch,
         ``model/minillm.py:76-106``); writes every layer's K/V into ``pool`` through the
-        requests' block tables and returns the last-token logits ``(n_prompts, vocab)``."""
+        requests' block tables and returns the last-token logits ``(n_prompts, vocab)``.
+        Projections are ``F.linear`` (thousands of rows); q/k norm + RoPE + the K/V write, each
+        residual add with the next RMSNorm and SiLU * up are one HIP launch each, as in
+        decode."""
         c = self.cfg
         lengths = [len(p) for p in prompts]
         cu = [0]
@@ -264,17 +252,20 @@ class Qwen3:
         sinks = [PagedWriteSink(pool, t, n) for t, n in zip(tables, lengths)]
         packed = PackedPrefill(cu_seqlens=cu, positions=positions, sinks=sinks)
         tokens = torch.tensor([t for p in prompts for t in p], dtype=torch.long, device=self.device)
-        x = F.embedding(tokens, self.w["embed"]).unsqueeze(0)  # (1, T, C)
-        cos, sin = self.cos[positions], self.sin[positions]
+        x = F.embedding(tokens, self.w["embed"])  # (T, C), the residual stream (updated in place)
+        T = x.shape[0]
+        _, h = add_rms_norm(x, None, self.w["l0.ln1"], c.eps)
         for i in range(c.n_layer):
-            h = rms_norm(x, self.w[f"l{i}.ln1"], c.eps)
-            q, k, v = self._qkv(i, h)
-            q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
-            packed.write(i, k, v)
+            p = f"l{i}."
+            # q/k norm + RoPE + the group's K/V write in one launch over one stacked projection
+            q, k, v = packed.write_rope(i, F.linear(h, self.w[p + "wqkv"]), self.w[p + "qn"], self.w[p + "kn"],
+                                        self.cos, self.sin, c.eps)
             y = packed.attend(q, k, v)
-            x = x + F.linear(y.reshape(1, -1, c.n_head * c.head_dim), self.w[f"l{i}.wo"])
-            x = x + self._mlp(i, rms_norm(x, self.w[f"l{i}.ln2"], c.eps))
-        return self.logits(x[0, packed.last_token_index])
+            _, h = add_rms_norm(x, F.linear(y.reshape(T, -1), self.w[p + "wo"]), self.w[p + "ln2"], c.eps)
+            m = silu_mul(F.linear(h, self.w[p + "wgu"]))
+            nxt = self.w[f"l{i + 1}.ln1"] if i + 1 < c.n_layer else self.w["norm"]
+            _, h = add_rms_norm(x, F.linear(m, self.w[p + "wd"]), nxt, c.eps)
+        return F.linear(h[packed.last_token_index], self.w["embed"])
 
     # ------------------------------------------------------------------ decode
     def _decode_stack(self, x: torch.Tensor, attend, h0: torch.Tensor | None = None) -> torch.Tensor:

@@ -101,6 +101,49 @@ def test_epilogue_validates_shapes():
         pool.write_qk_norm_rope(0, slots, qkv, qn, kn, cos[:, 1:], sin[:, 1:], pos, 1e-6)
 
 
+def test_packed_prefill_epilogue_matches_the_tensor_ops():
+    """PackedPrefill.write_rope: one launch for a packed group's q/k norm + RoPE at each
+    token's request-local position, the group's K/V write and the packed k/v the attention
+    reads; against the reference's ops (norms, apply_rotary_emb, write_prefill_slots)."""
+    from miattn import PackedPrefill, PagedWriteSink
+
+    H, H_kv, D, dtype, eps = 16, 8, 128, torch.bfloat16, 1e-6
+    lengths = [100, 37, 260]
+    T = sum(lengths)
+    g = torch.Generator().manual_seed(21)
+    qkv = (torch.randn(T, (H + 2 * H_kv) * D, generator=g) * 2.0).to(dtype).cuda()
+    qn = (1.0 + 0.1 * torch.randn(D, generator=g)).to(dtype).cuda()
+    kn = (1.0 + 0.1 * torch.randn(D, generator=g)).to(dtype).cuda()
+    cos, sin = rope_table(D, 1e6, 4096, "cuda", dtype)
+    perm = torch.randperm(64, generator=g).tolist()
+    tables, at = [], 0
+    for n in lengths:
+        nb = (n + 15) // 16
+        tables.append(perm[at:at + nb])
+        at += nb
+    positions = torch.cat([torch.arange(n) for n in lengths]).cuda()
+    cu = [0]
+    for n in lengths:
+        cu.append(cu[-1] + n)
+    pools = [PagedPool(1, 64, 16, H_kv, D, dtype=dtype, device="cuda", n_head=H, strict_writes=True)
+             for _ in range(2)]
+    packed = PackedPrefill(cu_seqlens=cu, positions=positions,
+                           sinks=[PagedWriteSink(pools[0], t, n) for t, n in zip(tables, lengths)])
+    q, k, v = packed.write_rope(0, qkv, qn, kn, cos, sin, eps)
+    slots = packed._packed_slots[1]
+    q_ref = _reference(pools[1], 0, qkv, qn, kn, cos, sin, positions, slots, H, H_kv, D, eps)
+    torch.cuda.synchronize()
+    assert q.shape == (1, T, H, D) and k.shape == (1, T, H_kv, D) and v.shape == (1, T, H_kv, D)
+    assert (q[0] == q_ref).float().mean().item() > 0.999 and _ulps(q[0], q_ref, dtype) <= 2.0
+    keys, vals = pools[0].keys[0].view(-1, H_kv, D), pools[0].values[0].view(-1, H_kv, D)
+    assert torch.equal(keys[slots], k[0]) and torch.equal(vals[slots], v[0])  # packed copies = pool rows
+    assert torch.equal(v[0], qkv[:, (H + H_kv) * D:].view(T, H_kv, D))
+    ref_keys = pools[1].keys[0].view(-1, H_kv, D)[slots]
+    assert (k[0] == ref_keys).float().mean().item() > 0.999 and _ulps(k[0], ref_keys, dtype) <= 2.0
+    with pytest.raises(RuntimeError, match="already written"):
+        packed.write_rope(0, qkv, qn, kn, cos, sin, eps)
+
+
 # ---------------------------------------------------------------- decode-step small ops
 from miattn.qwen3 import add_rms_norm, silu_mul  # noqa: E402
 import torch.nn.functional as F  # noqa: E402
