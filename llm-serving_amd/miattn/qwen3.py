@@ -157,8 +157,9 @@ def decode_step_begin(tokens: torch.Tensor, pos: torch.Tensor, table: torch.Tens
     V, C = embed.shape
     for name, t, dt in (("tokens", tokens, torch.int64), ("pos", pos, torch.int64), ("slots", slots, torch.int64),
                         ("seqlen", seqlen, torch.int32), ("error", error, torch.int32)):
-        if t.dtype != dt or not t.is_contiguous() or (name != "error" and t.numel() != B):
-            raise ValueError(f"{name} must be a contiguous {dt} tensor of {B} rows")
+        if t.dtype != dt or not t.is_contiguous() or (t.numel() < 1 if name == "error" else t.numel() != B):
+            raise ValueError(f"{name} must be a contiguous {dt} tensor of {'at least 1' if name == 'error' else B} "
+                             f"{'word' if name == 'error' else 'rows'}")
     if table.dtype != torch.int32 or table.dim() != 2 or table.shape[0] != B or table.stride(1) != 1:
         raise ValueError("table must be an int32 (B, max_blocks) block table with contiguous rows")
     for name, t in (("x", x), ("h", h)):
@@ -414,3 +415,11 @@ class GraphDecoder:
             self._step()
         else:
             self.graph.replay()
+
+    def check(self) -> None:
+        """Raise ``IndexError`` if a step met a token outside the vocabulary or a position
+        outside its row's block table (that row was skipped); one host synchronisation."""
+        bad = int(self.error.item())
+        if bad:
+            self.error.zero_()
+            raise IndexError(f"row {bad - 1}: token or position out of range in a decode step; the row was skipped")

@@ -100,6 +100,7 @@ def _free_run(model, use_graph):
         for _ in range(STEPS):
             dec.step()
         torch.cuda.synchronize()
+        dec.check()
         rest = dec.history.cpu()
     else:
         paged = PagedKV(pool, tables, lengths, rope_len=max(lengths) + STEPS + 1, n_head=model.cfg.n_head)
