@@ -182,13 +182,6 @@ def test_swiglu_launch_equals_projection_then_silu_mul(M, inter, K, dtype):
     assert ((got.float() - ref.float()).abs() <= 0.02 * ref.float().abs() + 1e-3).all()
 
 
-def test_glu_weight_interleaves_by_16():
-    wg = torch.arange(32 * 4, dtype=torch.float32).view(32, 4)
-    wu = -wg
-    w = glu_weight(wg, wu)
-    assert torch.equal(w[0:16], wg[0:16]) and torch.equal(w[16:32], wu[0:16])
-    assert torch.equal(w[32:48], wg[16:32]) and torch.equal(w[48:64], wu[16:32])
-
 
 def test_decode_step_begin_matches_the_tensor_ops():
     g = torch.Generator().manual_seed(11)
@@ -292,4 +285,3 @@ def test_tile_picks_follow_torch_on_ties_and_nan():
         torch.cuda.synchronize()
         assert tokens.cpu().tolist() == want
         assert torch.equal(tokens.cpu(), (xb.float() @ weight.float().t()).to(torch.bfloat16).cpu().argmax(-1))
-

@@ -157,3 +157,38 @@ def test_block_manager_contract():
 
 def test_availability_flag_is_exported():
     assert miattn.TRITON_AVAILABLE is miattn.HIP_AVAILABLE
+
+
+# ---------------------------------------------------------------- decode-step host helpers
+def test_glu_weight_interleaves_gate_and_up_rows_by_16():
+    from miattn.rows import glu_weight
+
+    wg = torch.arange(48 * 4, dtype=torch.float32).view(48, 4)
+    wu = -wg - 1
+    w = glu_weight(wg, wu)
+    assert w.shape == (96, 4)
+    for t in range(3):
+        assert torch.equal(w[32 * t:32 * t + 16], wg[16 * t:16 * t + 16])
+        assert torch.equal(w[32 * t + 16:32 * t + 32], wu[16 * t:16 * t + 16])
+    with pytest.raises(ValueError, match="inter % 16"):
+        glu_weight(wg[:40], wu[:40])
+
+
+def test_parts_hold_split_partials_and_sum_them_in_order():
+    from miattn.rows import Parts
+
+    data = torch.tensor([[[1e8, 1.0]], [[-1e8, 1.0]], [[1.0, 1.0]]], dtype=torch.float32)
+    p = Parts(data, torch.bfloat16)
+    assert p.shape == (1, 2) and p.n_parts == 3
+    # split order: (1e8 + -1e8) + 1 = 1 exactly, where another order could lose the 1
+    assert torch.equal(p.value(), torch.tensor([[1.0, 3.0]], dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="fp32"):
+        Parts(data.double(), torch.bfloat16)
+
+
+def test_rows_gemm_takes_only_device_tensors_of_its_shapes():
+    from miattn.rows import rows_supported
+
+    x = torch.zeros(4, 1024, dtype=torch.bfloat16)
+    w = torch.zeros(64, 1024, dtype=torch.bfloat16)
+    assert not rows_supported(x, w)  # host tensors: the product path is the HIP launch only
