@@ -18,8 +18,12 @@
  *   mi_silu_mul                                (reference model/layers.py:365-367, :342-350,
  *                                              :325-335)
  *   mi_rows_gemm       decode-step projections nn.Linear at a few rows: q/k/v, o, gate/up,
- *                                              down, lm_head (reference model/layers.py:176-222,
+ *   (+ _glu, _argmax)                          down, lm_head (reference model/layers.py:176-222,
  *                                              :325-335; model/minillm.py lm_head)
+ *   mi_decode_step_begin, decode-step          slot map + seqlen + embedding + layer-0 norm;
+ *   mi_greedy_advance(_tiles), bookkeeping     greedy argmax, tokens, history, positions
+ *   mi_argmax_rows                             (reference model/paged.py:474-501, the
+ *                                              generate loop's argmax)
  *
  * Conventions shared by every entry point:
  *   - every pointer except the `host_*` arguments is a device pointer;
