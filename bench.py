@@ -105,7 +105,9 @@ def decode_bytes(lengths, B, H, H_kv, D, max_blocks, esize=2) -> int:
     return kv + qo + meta
 
 
-def bench_decode(inp, steps: int, warmup: int, stream, eager: bool = False):
+def bench_decode(inp, steps: int, warmup: int, stream, eager: bool = False, check_rows=None):
+    """Time 28-layer decode steps; layer 0's output rows ``check_rows`` (default: all) are
+    checked against the fp32 oracle after the warm-up and before the timed region."""
     from miattn import paged_decode_plan
 
     B, H, D = inp.q[0].shape
@@ -127,6 +129,7 @@ def bench_decode(inp, steps: int, warmup: int, stream, eager: bool = False):
             step()
         torch.cuda.synchronize()
     eager_ms = (time.perf_counter() - t0) * 1e3 / (10 if not eager else steps)
+    checked = check_decode_rows(inp, outs[0], list(range(B)) if check_rows is None else check_rows)
     nbytes = decode_bytes(inp.lengths, B, H, H_kv, D, inp.block_table.shape[1])
     if eager:
         ms_per_step, per_step = eager_ms, [eager_ms]
@@ -141,6 +144,7 @@ def bench_decode(inp, steps: int, warmup: int, stream, eager: bool = False):
         "us_per_layer": ms_per_step * 1e3 / N_LAYER,
         "gbs": nbytes * N_LAYER / (ms_per_step * 1e-3) / 1e9,
         "out0": outs[0],
+        "checked_max_abs_diff": checked,
     }
 
 
@@ -150,11 +154,18 @@ def bench_prefill(stream, steps: int = 20, eager: bool = False):
     from miattn import HipVarlen, PackedPrefill, PagedPool, PagedWriteSink
     from miattn import workloads as W
 
+    from oracle.varlen import longhand_varlen
+
     inp = W.prefill_config3(device="cuda")
     backend = HipVarlen()
     H, D = inp.q.shape[1], inp.q.shape[2]
     flop = 4 * H * D * sum(n * (n + 1) // 2 for n in inp.lengths)  # causal pairs incl. diagonal
     ms = max(inp.lengths)
+    # checked against the fp32 longhand oracle before it is timed
+    got = backend.prefill_varlen(inp.q, inp.k, inp.v, cu_seqlens=inp.cu_seqlens, max_seqlen=ms).cpu().float()
+    prefill_diff = (got - longhand_varlen(inp.q.cpu(), inp.k.cpu(), inp.v.cpu(), inp.cu_seqlens)).abs().max().item()
+    if not prefill_diff <= 2e-2:
+        raise SystemExit(f"packed prefill disagrees with the oracle: max|delta|={prefill_diff}")
 
     def prefill_step():
         for _ in range(N_LAYER):
@@ -178,7 +189,7 @@ def bench_prefill(stream, steps: int = 20, eager: bool = False):
     positions = torch.cat([torch.arange(n) for n in inp.lengths]).cuda()
     sinks = [PagedWriteSink(pool, t_, n) for t_, n in zip(inp.tables, inp.lengths)]
     packed = PackedPrefill(cu_seqlens=inp.cu_seqlens, positions=positions, sinks=sinks, backend=backend)
-    slots = packed._packed_slots[1]
+    slots = packed.group_slots
     # distinct K/V sources per layer, so no layer's write reads what the previous one cached
     ks = [torch.randn_like(inp.k) for _ in range(N_LAYER)]
     vs = [torch.randn_like(inp.v) for _ in range(N_LAYER)]
@@ -186,6 +197,15 @@ def bench_prefill(stream, steps: int = 20, eager: bool = False):
     def write_step():
         for layer in range(N_LAYER):
             pool.write_prefill_slots(layer, slots, ks[layer], vs[layer])
+
+    # bit-exact before it is timed: every written slot row equals its source row
+    write_step()
+    pool.check_writes()
+    for layer in (0, N_LAYER - 1):
+        flat_k = pool.keys[layer].view(-1, *ks[layer].shape[1:])
+        flat_v = pool.values[layer].view(-1, *vs[layer].shape[1:])
+        if not (torch.equal(flat_k[slots], ks[layer]) and torch.equal(flat_v[slots], vs[layer])):
+            raise SystemExit(f"packed slot write is not bit-exact on layer {layer}")
 
     if eager:
         with torch.cuda.stream(stream):
@@ -211,6 +231,7 @@ def bench_prefill(stream, steps: int = 20, eager: bool = False):
         "slot_write_gbs": write_bytes / (write_ms * 1e-3) / 1e9,
         "slot_write_frac_hbm_peak": write_bytes / (write_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "slot_write_bytes_per_layer": write_bytes,
+        "checked": {"prefill_max_abs_diff_vs_fp32_oracle": prefill_diff, "slot_write_bit_exact": True},
     }
 
 
@@ -323,12 +344,29 @@ def copy_calibration(mib: int, reps: int) -> dict:
             "gbs_read_plus_write": 2 * n * 2 / dt / 1e9}
 
 
+def check_decode_rows(inp, out0, rows) -> float:
+    """Layer 0's output rows ``rows`` against the fp32 gather oracle (oracle.decode), before
+    anything is timed; returns max|delta| and exits when it is outside the bf16 bar."""
+    from oracle.decode import reference_paged_decode
+
+    idx = torch.tensor(rows)
+    got = out0.index_select(0, idx.to(out0.device)).cpu().float()
+    table = inp.block_table.cpu()[idx]
+    width = int(((inp.seqlen.cpu()[idx].max() + inp.block_size - 1) // inp.block_size).item())
+    expected = reference_paged_decode(inp.q[0].cpu()[idx], inp.k_caches[0].cpu(), inp.v_caches[0].cpu(),
+                                      table[:, :max(width, 1)], inp.seqlen.cpu()[idx], out_dtype=torch.float32)
+    diff = (got - expected).abs().max().item()
+    if not diff <= 2e-2:
+        raise SystemExit(f"paged decode disagrees with the oracle on rows {rows}: max|delta|={diff}")
+    return diff
+
+
 def bench_long_context(stream, steps: int = 10):
     from miattn import workloads as W
 
     inp = W.paged_decode_config(B=32, lengths=[8192] * 32, n_blocks=16384, n_layer=N_LAYER, device="cuda",
                                 max_blocks=512, seed=4)
-    res = bench_decode(inp, steps, 3, stream)
+    res = bench_decode(inp, steps, 3, stream, check_rows=[0, 13, 31])
     res.pop("out0")
     del inp
     torch.cuda.empty_cache()

@@ -90,9 +90,13 @@ int mi_kv_slot_write(const void* k, const void* v, const void* slot_ids, int slo
  *     q_out[b, h]           = rope(rmsnorm(q[b, h], q_norm_w), pos[b])       (B, H, D) contiguous
  *     k_pool_flat[slot[b]]  = rope(rmsnorm(k[b, :], k_norm_w), pos[b])
  *     v_pool_flat[slot[b]]  = v[b, :]
- * rmsnorm(x, w) = x / sqrt(mean(x^2) + eps) * w and NeoX rope with the (n_pos, D/2) cos/sin
- * tables at row pos[b] (int64), computed with the reference's per-op rounding to the
- * activation dtype (see csrc/decode_epilogue.hip). slot_ids as for mi_kv_slot_write (int32 or
+ * norm_mode 0: rmsnorm(x, w) = x / sqrt(mean(x^2) + eps) * w with the reference's per-op
+ * rounding to the activation dtype (Qwen3, model/layers.py:342-350); norm_mode 1: Qwen3.5's
+ * zero-centred norm x * (1 / sqrt(mean(x^2) + eps)) * (1 + w) in fp32, rounded once
+ * (model/qwen35.py:67-89). rope: NeoX rotation of the first rotary_dim elements of each head
+ * (64, 128 or 256, <= D; the rest pass through, model/layers.py:91-117) with the
+ * (n_pos, rotary_dim/2) cos/sin tables at row pos[b] (int64), each product and sum rounded
+ * to the activation dtype (see csrc/decode_epilogue.hip). slot_ids as for mi_kv_slot_write (int32 or
  * int64 per slot_bits; pools (n_slots, H_kv, D) contiguous). A row whose position is outside
  * [0, n_pos) or whose slot is outside [0, n_slots) is not written and 1 + its index goes to
  * *error_word (may be NULL). D = 64, 128 or 256. qkv_parts = 0: qkv holds `dtype` values;
@@ -103,10 +107,10 @@ int mi_kv_slot_write(const void* k, const void* v, const void* slot_ids, int slo
  * attention then reading q_out, k_out, v_out (reference model/packed.py:187-218). */
 int mi_qk_norm_rope_write(const void* qkv, int64_t row_stride, int qkv_parts, const void* q_norm_w,
                           const void* k_norm_w, const void* cos_tab, const void* sin_tab,
-                          int64_t n_pos, const int64_t* pos, const void* slot_ids, int slot_bits,
-                          void* q_out, void* k_pool, void* v_pool, void* k_out, void* v_out, int B, int H,
-                          int H_kv, int D, int64_t n_slots, float eps, int dtype, int32_t* error_word,
-                          void* stream);
+                          int64_t n_pos, int rotary_dim, const int64_t* pos, const void* slot_ids,
+                          int slot_bits, void* q_out, void* k_pool, void* v_pool, void* k_out, void* v_out,
+                          int B, int H, int H_kv, int D, int64_t n_slots, float eps, int norm_mode, int dtype,
+                          int32_t* error_word, void* stream);
 
 /* ------------------------------------------------------------------ decode-step small ops
  * The residual stream's add + RMSNorm and the MLP's SiLU(gate) * up, each one launch (the
@@ -138,8 +142,11 @@ int mi_argmax_rows(const void* x, int64_t ld, int rows, int cols, int64_t* out, 
  * mi_decode_step_begin, per row b (block_table (B, >= max_blocks) int32, row stride bt_stride):
  *   seqlen[b] = pos[b] + 1;  slots[b] = table[b, pos[b] / block_size] * block_size + pos[b] % block_size;
  *   x[b] = embed[tokens[b]] (embed (vocab, cols));  h[b] = x[b] / sqrt(mean(x[b]^2) + eps) * norm_w,
- *   rounded as mi_add_rms_norm. A row whose token is outside [0, vocab) or whose position is
- *   outside its table is not written and 1 + its index goes to *error_word (may be NULL).
+ *   rounded as mi_add_rms_norm. A row whose token is outside [0, vocab), whose position is
+ *   outside [0, max_blocks * block_size) or whose table entry at that position is negative
+ *   (pad each row's table with -1 past its own blocks) is refused: 1 + its index goes to
+ *   *error_word (may be NULL) and the row is made inert for the step (seqlen 0, slot -1,
+ *   x = h = 0), so no later launch of the step writes or reads pool memory for it.
  * mi_greedy_advance: pick[r] = argmax of logits row r as mi_argmax_rows; tokens[r] = pick;
  *   history[r * hist_stride + steps[r]] = pick while 0 <= steps[r] < max_steps; steps[r] += 1;
  *   pos[r] += 1 (all int64). */
@@ -225,8 +232,8 @@ int mi_paged_decode(const void* q, const void* k_cache, const void* v_cache,
  * the LDS-ring kernel (128-row tiles), shorter ones the persistent duo kernel (64-row
  * tiles, two workgroups per CU, each working through its own item list), head_dim 256 the
  * register-staged kernel (64-row tiles); mi_varlen_schedule_for names the kernel instead
- * (MI_PREFILL_*; the ring, wide and duo kernels take head_dim 64 and 128 only). Layout of
- * the staged, ring and wide schedules:
+ * (MI_PREFILL_*; the ring and duo kernels take head_dim 64 and 128 only). Layout of
+ * the staged and ring schedules:
  * {n_work, n_merge, n_partials, layout}, then n_work work entries and n_merge merge
  * entries of two words each; the duo schedule is {n_workgroups, n_merge, n_partials,
  * layout}, n_workgroups {first item word, item count} pairs, the merge entries, then the
@@ -237,7 +244,7 @@ int mi_paged_decode(const void* q, const void* k_cache, const void* v_cache,
  * Split pieces write (O, max, sum) partials into the caller's workspace of
  * mi_varlen_workspace_size() bytes (0 when nothing is split; 16-byte aligned); a second
  * launch on the same stream merges them. Calls sharing a workspace must be ordered. */
-enum { MI_PREFILL_AUTO = -1, MI_PREFILL_STAGED = 0, MI_PREFILL_RING = 1, MI_PREFILL_WIDE = 2, MI_PREFILL_DUO = 3 };
+enum { MI_PREFILL_AUTO = -1, MI_PREFILL_STAGED = 0, MI_PREFILL_RING = 1, MI_PREFILL_DUO = 3 };
 int mi_varlen_schedule(const int32_t* host_cu_seqlens, int n_seqs, int H, int H_kv,
                        int D, int causal, int32_t* host_schedule, int capacity);
 int mi_varlen_schedule_for(const int32_t* host_cu_seqlens, int n_seqs, int H, int H_kv,

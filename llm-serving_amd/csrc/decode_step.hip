@@ -125,9 +125,14 @@ __global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(
 
 // Start of a captured decode step, one workgroup per row: seqlen = pos + 1, the row's write
 // slot table[pos / bs] * bs + pos % bs (reference model/paged.py:499-501), x = embed[token]
-// (the embedding lookup) and h = rmsnorm(x) * w (layer 0's input norm). A row whose token is
-// outside the vocabulary or whose position is outside its block table is left unwritten
-// and reported (row + 1) through the error word.
+// (the embedding lookup) and h = rmsnorm(x) * w (layer 0's input norm).
+// A row is refused when its token is outside the vocabulary, its position is negative or
+// past the table's width, or the table entry for its position is negative (a row's table
+// padded with -1 past its own blocks, so a row that runs past its own blocks is caught
+// even inside a wider batch table). A refused row is reported (row + 1) through the error
+// word and made inert for the rest of the step: slot -1 (every later write of the row is
+// skipped and reported by its own launch), seqlen 0 (its attention reads nothing and is
+// zero) and x = h = 0; no other row's state is touched.
 template <typename T, int PER>
 __global__ __launch_bounds__(kNormThreads) void step_begin_kernel(
     const int64_t* __restrict__ tokens, const int64_t* __restrict__ pos, const int32_t* __restrict__ table,
@@ -138,13 +143,23 @@ __global__ __launch_bounds__(kNormThreads) void step_begin_kernel(
   const int tid = threadIdx.x;
   const int64_t t = tokens[row];
   const int64_t p = pos[row];
-  if (t < 0 || t >= vocab || p < 0 || p / block_size >= max_blocks) {  // uniform over the workgroup
-    if (tid == 0 && err != nullptr) atomicCAS(err, 0, row + 1);
+  const bool in_table = p >= 0 && p / block_size < max_blocks;
+  const int32_t page = in_table ? table[row * bt_stride + p / block_size] : -1;
+  if (t < 0 || t >= vocab || page < 0) {  // uniform over the workgroup
+    if (tid == 0) {
+      if (err != nullptr) atomicCAS(err, 0, row + 1);
+      seqlen[row] = 0;
+      slots[row] = -1;
+    }
+    for (int i = tid; i < cols; i += kNormThreads) {
+      x[int64_t(row) * cols + i] = from_f32<T>(0.0f);
+      h[int64_t(row) * cols + i] = from_f32<T>(0.0f);
+    }
     return;
   }
   if (tid == 0) {
     seqlen[row] = int32_t(p + 1);
-    slots[row] = int64_t(table[row * bt_stride + p / block_size]) * block_size + p % block_size;
+    slots[row] = int64_t(page) * block_size + p % block_size;
   }
   const T* er = embed + t * cols;
   float s[PER], wv[PER];

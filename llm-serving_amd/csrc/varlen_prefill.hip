@@ -947,388 +947,6 @@ __global__ __launch_bounds__(Ring<D>::THREADS, 1) void varlen_prefill_ring_kerne
   }
 }
 
-// ---------------------------------------------------------------- wide kernel (D = 64, 128)
-// Four waves, one per SIMD, own 64 query rows; each wave computes all 64 rows (two blocks
-// of 32) against its quarter (32 keys) of every 128-key step, so each K fragment and each
-// V^T fragment it reads from LDS feeds two MFMAs: half the LDS read traffic per FLOP of a
-// 32-row wave, which on gfx950 is what bounds a step (a wave-step of 32 rows x 32 keys
-// reads 16 KiB of operands for 16 MFMAs). The 64-row tile keeps the batch finely divided
-// for load balance, and the four key quarters halve the serial chain of the longest
-// causal tile against a 64-key step.
-//
-// K and V stream into two LDS rings of two 128-key buffers each (buffer_load_dwordx4 ...
-// lds; 16-byte chunks swizzled as in the ring kernel). Step it computes the softmax of
-// tile t (scores in registers), the scores of tile t+1 (K(t+1) resident) and PV of tile t
-// (V(t) resident) while K(t+2) and V(t+1) land in the buffers K(t) and V(t-1) left; one
-// barrier per step. The four key quarters of each query row are folded at the end through
-// LDS, each wave normalising and storing one 32-wide block of head dims.
-template <int D>
-struct Wide {
-  static constexpr int WAVES = 4;             // key quarters of a step
-  static constexpr int THREADS = 64 * WAVES;
-  static constexpr int QPW = 2;               // query blocks of 32 per wave
-  static constexpr int BQ = 32 * QPW;         // query rows per workgroup
-  static constexpr int BK = 32 * WAVES;       // keys per step
-  static constexpr int ROWB = D * 2;          // bytes of one key row of one KV head
-  static constexpr int NCH = D / 8;           // 16-byte chunks per row
-  static constexpr int BUFB = BK * ROWB;      // bytes of one K (or V) buffer
-  static constexpr int SEGS = BUFB / 1024;    // 1 KiB wave-wide loads per buffer
-  static constexpr int LPW = SEGS / WAVES;    // of them per wave
-  static constexpr int RPS = 1024 / ROWB;     // key rows per wave-wide load
-  static constexpr int SWB = NCH == 16 ? 4 : 3;
-  static_assert(D == 64 || D == 128, "wide kernel head dims");
-  static_assert(SEGS % WAVES == 0, "whole loads per wave");
-  static_assert(WAVES * QPW * (D / 32) * 16 * 64 * 4 <= 4 * BUFB, "fold fits the rings");
-  static __device__ __forceinline__ int sw(int r) {
-    return ((r & 3) << (SWB - 2)) | ((r >> 2) & ((NCH >> 2) - 1));
-  }
-};
-
-template <typename T, int D>
-__global__ __launch_bounds__(Wide<D>::THREADS, 1) void varlen_prefill_wide_kernel(
-    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
-    T* __restrict__ out, const int32_t* __restrict__ cu, const int32_t* __restrict__ sched,
-    float* __restrict__ partials, int H, int H_kv, int G, float scale_log2, int causal) {
-  using W = Wide<D>;
-  constexpr int KS = D / 16;  // MFMA k-steps over D for S^T
-  constexpr int DB = D / 32;  // 32-row blocks of D for O^T
-  constexpr int QPW = W::QPW, BK = W::BK, BQ = W::BQ, ROWB = W::ROWB, LPW = W::LPW;
-  // Separately declared buffers, so the compiler's wait insertion tells their loads apart.
-  __shared__ __align__(16) uint8_t kb0[W::BUFB];
-  __shared__ __align__(16) uint8_t kb1[W::BUFB];
-  __shared__ __align__(16) uint8_t vb0[W::BUFB];
-  __shared__ __align__(16) uint8_t vb1[W::BUFB];
-  __shared__ float mlx[W::WAVES][QPW][2][64];  // (m, l) of every wave, for the fold
-
-  const int x = blockIdx.x;
-  const int h = (H % kXcds == 0) ? (x % kXcds) * (H / kXcds) + x / kXcds : x;
-  const int kvh = h / G;
-  // work entry: (seq << 16 | tile, split << 28 | (n_split - 1) << 24 | partial slot)
-  const int entry = sched[2 * blockIdx.y];
-  const int piece = sched[2 * blockIdx.y + 1];
-  const int seq = int(uint32_t(entry) >> 16);
-  const int tile = entry & 0xffff;
-  const int split = int(uint32_t(piece) >> 28);
-  const int n_split = ((piece >> 24) & 15) + 1;
-  const int slot = piece & 0xffffff;
-  const int seq0 = cu[seq];
-  const int L = cu[seq + 1] - seq0;
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int kq = __builtin_amdgcn_readfirstlane(tid >> 6);  // key quarter of every step
-  const int g = lane >> 5;
-  const int col = lane & 31;
-  const int row0 = tile * BQ;
-  int qi[QPW];
-#pragma unroll
-  for (int j = 0; j < QPW; ++j) qi[j] = row0 + j * 32 + col;
-
-  const int64_t q_row = int64_t(H) * D;
-  const int64_t kv_row_b = int64_t(H_kv) * ROWB;
-
-  const int q_end = min(L, row0 + BQ);
-  const int n_all = causal ? (q_end + BK - 1) / BK : (L + BK - 1) / BK;
-  const int t_first = split * n_all / n_split;
-  const int t_end = (split + 1) * n_all / n_split;
-  const int n_it = t_end - t_first;
-
-  uint4 qB[QPW][KS];
-#pragma unroll
-  for (int j = 0; j < QPW; ++j) {
-    const int qc = qi[j] < L ? qi[j] : L - 1;
-    const T* qp_ = q + int64_t(seq0 + qc) * q_row + h * D + g * 8;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qB[j][ks] = load16(qp_ + ks * 16);
-  }
-
-  // Wave-wide load i of this wave fills 1 KiB segment kq + i * WAVES of a buffer: lane t
-  // writes bytes 16t.. of it, i.e. key row (kq + i * WAVES) * RPS + t / NCH, slot t % NCH,
-  // which holds chunk slot ^ sw(row) of that row. sw(row) does not depend on i (load i's
-  // rows are load 0's plus i * WAVES * RPS, which leaves both swizzle fields unchanged), so
-  // one lane offset serves every load; load i's buffer resource starts i * WAVES * RPS rows
-  // further on (its range check then still ends exactly at the segment's last token).
-  static_assert((W::WAVES * W::RPS) % W::NCH == 0, "swizzle invariant across a wave's loads");
-  const int dma_r0 = kq * W::RPS + lane / W::NCH;
-  const int dma_off = int(dma_r0 * kv_row_b) + kvh * ROWB + (((lane % W::NCH) ^ W::sw(dma_r0)) << 4);
-  const int dma_rows = W::WAVES * W::RPS;
-  const char* kseg = reinterpret_cast<const char*>(k) + int64_t(seq0) * kv_row_b;
-  const char* vseg = reinterpret_cast<const char*>(v) + int64_t(seq0) * kv_row_b;
-  // Load i of step tile t: base = token t * BK + i * dma_rows, size = up to the segment's
-  // end (rows past it read as zero); tiles past this piece get an empty range.
-  auto issue = [&](const char* seg, int t, uint8_t* dst) {
-#pragma unroll
-    for (int i = 0; i < LPW; ++i) {
-      const int first = t * BK + i * dma_rows;
-      const int rem = t < t_end ? min(L - first, dma_rows) : 0;  // rows this load may read
-      const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(seg + int64_t(first) * kv_row_b), (short)0,
-                                                        rem > 0 ? rem * int(kv_row_b) : 0, 0x00020000);
-      buffer_load_lds16(rs, (lds_void_t*)((__attribute__((address_space(3))) uint8_t*)dst + (kq + i * W::WAVES) * 1024),
-                        dma_off);
-    }
-  };
-
-  // Loop-invariant LDS byte offsets of this lane's operands within a buffer: K fragment of
-  // k-step ks (key row kq*32 + col, elements ks*16 + 8g ..) and the two transposed reads of
-  // each V^T operand (k-step t2 of the wave's 32 keys, head-dim block db), laid out as in
-  // the ring kernel so the V^T key order matches the score accumulator's.
-  int k_rd[KS];
-  {
-    const int r = kq * 32 + col;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) k_rd[ks] = r * ROWB + (((ks * 2 + g) ^ W::sw(r)) << 4);
-  }
-  int v_rd[DB][2][2];
-#pragma unroll
-  for (int db = 0; db < DB; ++db) {
-#pragma unroll
-    for (int t2 = 0; t2 < 2; ++t2) {
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const int key = kq * 32 + 16 * t2 + 8 * hh + 4 * g + ((lane & 15) >> 2);
-        const int d0 = db * 32 + ((lane >> 4) & 1) * 16 + 4 * (lane & 3);
-        v_rd[db][t2][hh] = key * ROWB + (((d0 >> 3) ^ W::sw(key)) << 4) + ((d0 >> 2) & 1) * 8;
-      }
-    }
-  }
-
-  floatx16 o[QPW][DB];
-  float m_i[QPW], l_i[QPW];
-#pragma unroll
-  for (int j = 0; j < QPW; ++j) {
-#pragma unroll
-    for (int i = 0; i < DB; ++i) o[j][i] = zero16();
-    m_i[j] = -INFINITY;
-    l_i[j] = 0.0f;
-  }
-
-  auto kfrags = [&](const uint8_t* kb, uint4 (&kf)[KS]) {
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) kf[ks] = *reinterpret_cast<const uint4*>(kb + k_rd[ks]);
-  };
-  auto scores = [&](const uint4 (&kf)[KS], floatx16 (&s)[QPW]) {
-#pragma unroll
-    for (int j = 0; j < QPW; ++j) {
-      floatx16 a = zero16();
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) a = mfma32<T>(kf[ks], qB[j][ks], a);
-      s[j] = a;
-    }
-  };
-
-  // Prologue: K(t0) -> kb0, K(t0+1) -> kb1, V(t0) -> vb0; scores of t0 once K(t0) landed.
-  issue(kseg, t_first, kb0);
-  issue(kseg, t_first + 1, kb1);
-  issue(vseg, t_first, vb0);
-#pragma unroll
-  for (int j = 0; j < QPW; ++j) {
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      asm volatile("" ::"v"(qB[j][ks].x), "v"(qB[j][ks].y), "v"(qB[j][ks].z), "v"(qB[j][ks].w));
-    }
-  }
-  wait_vm_lgkm0<2 * LPW>();
-  bare_barrier();
-  floatx16 cur[QPW], nxt[QPW];
-  {
-    uint4 kf[KS];
-    kfrags(kb0, kf);
-    scores(kf, cur);
-  }
-  wait_vm_lgkm0<0>();
-  bare_barrier();
-
-  // One step. KB: buffer holding K(t+1) (read) -- K(t+2) goes to the other one, which
-  // held K(t); VB: buffer holding V(t) (read) -- V(t+1) goes to the other one.
-  auto step = [&](int it, uint8_t* kb_next, uint8_t* kb_free, uint8_t* vb_cur, uint8_t* vb_free, auto mask_c) {
-    constexpr bool kMask = decltype(mask_c)::value;
-    const int t = t_first + it;
-    issue(kseg, t + 2, kb_free);
-    issue(vseg, t + 1, vb_free);
-    // online softmax of tile t for both query blocks (raw score units; scale folded into
-    // the exp2 argument), lazy rescaling as in the ring kernel
-    const int kb0_ = t * BK + kq * 32;
-    uint4 pB[QPW][2];
-    float alpha[QPW];
-    bool moved[QPW];
-#pragma unroll
-    for (int j = 0; j < QPW; ++j) {
-      floatx16 sc = cur[j];
-      if constexpr (kMask) {
-        const int lim = (causal ? min(L, qi[j] + 1) : L) - kb0_ - g * 4;  // key offsets < lim are valid
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          if ((e >> 2) * 8 + (e & 3) >= lim) sc[e] = -INFINITY;
-        }
-      }
-      float mloc = sc[0];
-#pragma unroll
-      for (int e = 1; e < 16; ++e) mloc = fmaxf(mloc, sc[e]);
-      const float m_tile = fmaxf(mloc, swap32(mloc)) * scale_log2;
-      moved[j] = __any(m_tile > m_i[j] + 8.0f);
-      const float m_new = moved[j] ? fmaxf(m_i[j], m_tile) : m_i[j];
-      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-      alpha[j] = fast_exp2(m_i[j] - m_use);
-      m_i[j] = m_new;
-      float lsum = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float p = fast_exp2(fmaf(sc[e], scale_log2, -m_use));
-        sc[e] = p;
-        lsum += p;
-      }
-      l_i[j] = fmaf(l_i[j], alpha[j], lsum);
-#pragma unroll
-      for (int t2 = 0; t2 < 2; ++t2) {
-        pB[j][t2] = make_uint4(pack2<T>(sc[8 * t2 + 0], sc[8 * t2 + 1]), pack2<T>(sc[8 * t2 + 2], sc[8 * t2 + 3]),
-                               pack2<T>(sc[8 * t2 + 4], sc[8 * t2 + 5]), pack2<T>(sc[8 * t2 + 6], sc[8 * t2 + 7]));
-      }
-    }
-    // scores of tile t+1, each K fragment read from LDS feeding both query blocks
-#pragma unroll
-    for (int j = 0; j < QPW; ++j) nxt[j] = zero16();
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const uint4 kf = *reinterpret_cast<const uint4*>(kb_next + k_rd[ks]);
-#pragma unroll
-      for (int j = 0; j < QPW; ++j) nxt[j] = mfma32<T>(kf, qB[j][ks], nxt[j]);
-    }
-#pragma unroll
-    for (int j = 0; j < QPW; ++j) {
-      if (moved[j]) {
-#pragma unroll
-        for (int i = 0; i < DB; ++i) o[j][i] *= alpha[j];
-      }
-    }
-    // PV of tile t, each V^T fragment feeding both query blocks
-#pragma unroll
-    for (int db = 0; db < DB; ++db) {
-#pragma unroll
-      for (int t2 = 0; t2 < 2; ++t2) {
-        const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_short4_t*)((__attribute__((address_space(3))) const uint8_t*)vb_cur + v_rd[db][t2][0]));
-        const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_short4_t*)((__attribute__((address_space(3))) const uint8_t*)vb_cur + v_rd[db][t2][1]));
-        const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
-        const uint4 vf = make_uint4(l2.x, l2.y, h2.x, h2.y);
-#pragma unroll
-        for (int j = 0; j < QPW; ++j) o[j][db] = mfma32<T>(vf, pB[j][t2], o[j][db]);
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < QPW; ++j) cur[j] = nxt[j];
-    wait_vm_lgkm0<0>();
-    bare_barrier();
-  };
-  // Every step runs the masked softmax (the compare-and-select is cheap next to the step's
-  // MFMAs; an unmasked copy of the step for interior tiles pushes the kernel past the
-  // register file and into scratch).
-  int it = 0;
-  for (; it + 2 <= n_it; it += 2) {
-    step(it, kb1, kb0, vb0, vb1, std::true_type{});
-    step(it + 1, kb0, kb1, vb1, vb0, std::true_type{});
-  }
-  if (it < n_it) step(it, kb1, kb0, vb0, vb1, std::true_type{});
-  // every wave's loads were waited for by the last step's barrier: the rings are free
-
-  // Fold the four key quarters: wave kq keeps head-dim block kq and receives it from the
-  // other waves; O^T blocks go through the rings as [e][lane] floats (conflict-free).
-  float l_tot[QPW];
-#pragma unroll
-  for (int j = 0; j < QPW; ++j) {
-    l_tot[j] = l_i[j] + swap32(l_i[j]);
-    mlx[kq][j][0][lane] = m_i[j];
-    mlx[kq][j][1][lane] = l_tot[j];
-  }
-  auto fold_slot = [&](int db, int w, int j) -> float* {
-    // (db, writer w, block j) -> 4 KiB slot; DB * WAVES * QPW slots over the four buffers
-    const int s = (db * W::WAVES + w) * QPW + j;
-    constexpr int per_buf = W::BUFB / (16 * 64 * 4);
-    uint8_t* b = s / per_buf == 0 ? kb0 : s / per_buf == 1 ? kb1 : s / per_buf == 2 ? vb0 : vb1;
-    return reinterpret_cast<float*>(b) + (s % per_buf) * (16 * 64);
-  };
-#pragma unroll
-  for (int db = 0; db < DB; ++db) {
-    if (db == kq) continue;
-#pragma unroll
-    for (int j = 0; j < QPW; ++j) {
-      float* dst = fold_slot(db, kq, j);
-#pragma unroll
-      for (int e = 0; e < 16; ++e) dst[e * 64 + lane] = o[j][db][e];
-    }
-  }
-  __syncthreads();
-  // head-dim blocks this wave finalises: kq (D = 128), or none / kq for D = 64 (DB = 2:
-  // waves 0 and 1 finalise blocks 0 and 1; waves 2 and 3 only contribute)
-  if (kq >= DB) return;
-  const int db = kq;
-#pragma unroll
-  for (int j = 0; j < QPW; ++j) {
-    float mw[W::WAVES];
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < W::WAVES; ++w) {
-      mw[w] = mlx[w][j][0][lane];
-      M = fmaxf(M, mw[w]);
-    }
-    const float M_use = M == -INFINITY ? 0.0f : M;
-    float wt[W::WAVES];
-    float l_all = 0.0f;
-#pragma unroll
-    for (int w = 0; w < W::WAVES; ++w) {
-      wt[w] = fast_exp2(mw[w] - M_use);
-      l_all = fmaf(mlx[w][j][1][lane], wt[w], l_all);
-    }
-    float r[16];
-#pragma unroll
-    for (int e = 0; e < 16; ++e) r[e] = 0.0f;
-#pragma unroll
-    for (int w = 0; w < W::WAVES; ++w) {
-      if (w == kq) {
-        // own block: registers (the compile-time index keeps o in registers)
-#pragma unroll
-        for (int dd = 0; dd < DB; ++dd) {
-          if (dd == db) {
-#pragma unroll
-            for (int e = 0; e < 16; ++e) r[e] = fmaf(o[j][dd][e], wt[w], r[e]);
-          }
-        }
-      } else {
-        const float* src = fold_slot(db, w, j);
-#pragma unroll
-        for (int e = 0; e < 16; ++e) r[e] = fmaf(src[e * 64 + lane], wt[w], r[e]);
-      }
-    }
-    const int qrow = qi[j];
-    if (n_split > 1) {
-      // this piece's (O relative to M, M, l) for the merge launch; rows past the segment
-      // are written too and never read
-      float* pbase = partials + (int64_t(slot + split) * H + h) * (BQ * (D + 2));
-      const int row = j * 32 + col;
-      float* prow = pbase + row * D;
-#pragma unroll
-      for (int jg = 0; jg < 4; ++jg) {
-        const int d = db * 32 + jg * 8 + g * 4;
-        *reinterpret_cast<float4*>(prow + d) =
-            make_float4(r[jg * 4 + 0], r[jg * 4 + 1], r[jg * 4 + 2], r[jg * 4 + 3]);
-      }
-      if (db == 0 && g == 0) *reinterpret_cast<float2*>(pbase + BQ * D + row * 2) = make_float2(M, l_all);
-      continue;
-    }
-    const float inv = 1.0f / fmaxf(l_all, 1e-30f);
-    if (qrow < L) {
-      T* op = out + int64_t(seq0 + qrow) * q_row + h * D;
-#pragma unroll
-      for (int jg = 0; jg < 4; ++jg) {
-        const int d = db * 32 + jg * 8 + g * 4;
-        const uint2 val = make_uint2(pack2<T>(r[jg * 4 + 0] * inv, r[jg * 4 + 1] * inv),
-                                     pack2<T>(r[jg * 4 + 2] * inv, r[jg * 4 + 3] * inv));
-        *reinterpret_cast<uint2*>(op + d) = val;
-      }
-    }
-  }
-}
-
 // ---------------------------------------------------------------- duo kernel (D = 64, 128)
 // Persistent: the grid is two workgroups per CU, and each works through its own list of
 // items (a 64-row query tile, or a key-range piece of one, of one head), which the host
@@ -1850,20 +1468,19 @@ __global__ __launch_bounds__(256) void varlen_prefill_merge_kernel(
 }
 
 // Schedule layout word: kernel kind << 20 | head_dim << 8 | query rows per tile.
-enum Kind { kStaged = MI_PREFILL_STAGED, kRing = MI_PREFILL_RING, kWide = MI_PREFILL_WIDE, kDuo = MI_PREFILL_DUO };
+enum Kind { kStaged = MI_PREFILL_STAGED, kRing = MI_PREFILL_RING, kDuo = MI_PREFILL_DUO };
 constexpr int layout_word(int kind, int D, int rows) { return (kind << 20) | (D << 8) | rows; }
 constexpr int layout_kind(int layout) { return layout >> 20; }
 constexpr int layout_d(int layout) { return (layout >> 8) & 0xfff; }
 constexpr int layout_rows(int layout) { return layout & 0xff; }
 int kind_rows(int kind) {
-  return kind == kRing ? Ring<128>::BQ : kind == kWide ? Wide<128>::BQ : kind == kDuo ? Duo<128>::BQ : kBQ;
+  return kind == kRing ? Ring<128>::BQ : kind == kDuo ? Duo<128>::BQ : kBQ;
 }
 // keys per schedule unit of work (a causal tile's cost is counted in these)
-int kind_keys(int kind) { return kind == kWide ? Wide<128>::BK : kind == kDuo ? Duo<128>::BK : Ring<128>::BK; }
+int kind_keys(int kind) { return kind == kDuo ? Duo<128>::BK : Ring<128>::BK; }
 // workgroups one CU holds at once
 int kind_per_cu(int kind) { return kind == kDuo || kind == kStaged ? 2 : 1; }
 static_assert(Ring<128>::BK == Tiles<256>::BK && Ring<64>::BK == Tiles<128>::BK, "64-key tiles");
-static_assert(Wide<64>::BQ == Wide<128>::BQ && Wide<64>::BK == Wide<128>::BK, "wide tile shape");
 static_assert(Duo<64>::BQ == Duo<128>::BQ && Duo<64>::BK == Duo<128>::BK, "duo tile shape");
 
 template <typename T, int D>
@@ -1872,7 +1489,7 @@ int launch2(const void* q, const void* k, const void* v, void* out, const int32_
             int H_kv, float scale_log2, int causal, hipStream_t s) {
   const int32_t* work = sched + kSchedHeader;
   if constexpr (D == 64 || D == 128) {
-    if (kind == kRing || kind == kWide || kind == kDuo) {
+    if (kind == kRing || kind == kDuo) {
       constexpr int kRowsPerBlock = 256 / (D / 32);
       if (kind == kRing) {
         hipLaunchKernelGGL((varlen_prefill_ring_kernel<T, D>), dim3(H, n_work), dim3(Ring<D>::THREADS), 0, s,
@@ -1892,15 +1509,6 @@ int launch2(const void* q, const void* k, const void* v, void* out, const int32_
         if (n_merge > 0) {
           hipLaunchKernelGGL((varlen_prefill_merge_kernel<T, D, Duo<D>::BQ>),
                              dim3(H, n_merge, (Duo<D>::BQ + kRowsPerBlock - 1) / kRowsPerBlock), dim3(256), 0, s,
-                             cu, work + 2 * n_work, static_cast<const float*>(partials), static_cast<T*>(out), H);
-        }
-      } else {
-        hipLaunchKernelGGL((varlen_prefill_wide_kernel<T, D>), dim3(H, n_work), dim3(Wide<D>::THREADS), 0, s,
-                           static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
-                           static_cast<T*>(out), cu, work, partials, H, H_kv, H / H_kv, scale_log2, causal);
-        if (n_merge > 0) {
-          hipLaunchKernelGGL((varlen_prefill_merge_kernel<T, D, Wide<D>::BQ>),
-                             dim3(H, n_merge, (Wide<D>::BQ + kRowsPerBlock - 1) / kRowsPerBlock), dim3(256), 0, s,
                              cu, work + 2 * n_work, static_cast<const float*>(partials), static_cast<T*>(out), H);
         }
       }
@@ -2013,11 +1621,11 @@ extern "C" int mi_varlen_schedule_for(const int32_t* host_cu_seqlens, int n_seqs
                                       int D, int causal, int kernel, int32_t* host_schedule,
                                       int capacity) {
   using namespace miattn;
-  if (kernel < MI_PREFILL_AUTO || kernel > MI_PREFILL_DUO) {
+  if (kernel < MI_PREFILL_AUTO || kernel > MI_PREFILL_DUO || kernel == 2) {
     return fail(MI_ERR_INVALID, "mi_varlen_schedule: unknown prefill kernel %d", kernel);
   }
   if (kernel != MI_PREFILL_AUTO && kernel != MI_PREFILL_STAGED && D != 64 && D != 128) {
-    return fail(MI_ERR_UNSUPPORTED, "mi_varlen_schedule: the ring and wide kernels take head_dim 64 or 128, got %d",
+    return fail(MI_ERR_UNSUPPORTED, "mi_varlen_schedule: the ring and duo kernels take head_dim 64 or 128, got %d",
                 D);
   }
   if (host_cu_seqlens == nullptr || n_seqs < 1 || n_seqs > 65535) {
@@ -2036,7 +1644,7 @@ extern "C" int mi_varlen_schedule_for(const int32_t* host_cu_seqlens, int n_seqs
   // kRingMinLen tokens and the persistent duo kernel otherwise (head_dim 256 runs the
   // register-staged kernel); the caller may name a kernel instead.
   const int kind = kernel == MI_PREFILL_STAGED ? kStaged : kernel == MI_PREFILL_RING ? kRing
-                 : kernel == MI_PREFILL_WIDE ? kWide : kernel == MI_PREFILL_DUO ? kDuo
+                 : kernel == MI_PREFILL_DUO ? kDuo
                  : (D == 64 || D == 128) ? (max_len >= kRingMinLen ? kRing : kDuo) : kStaged;
   const bool ring = kind != kStaged;  // one workgroup per CU, split-K capable
   const int RW = kind_rows(kind);
@@ -2144,8 +1752,8 @@ extern "C" int mi_varlen_prefill(const void* q, const void* k, const void* v, vo
   }
   const int rows = layout_rows(layout);
   const int kind = layout_kind(layout);
-  const bool split_capable = kind == kRing || kind == kWide || kind == kDuo;
-  if (layout_d(layout) != D || kind < kStaged || kind > kDuo || rows != kind_rows(kind) ||
+  const bool split_capable = kind == kRing || kind == kDuo;
+  if (layout_d(layout) != D || kind < kStaged || kind > kDuo || kind == 2 || rows != kind_rows(kind) ||
       (split_capable && D != 64 && D != 128) || (n_merge > 0) != (n_partials > 0) ||
       (n_merge > 0 && !split_capable)) {
     return fail(MI_ERR_INVALID, "mi_varlen_prefill: schedule (layout 0x%x) does not match head_dim %d",

@@ -4,26 +4,25 @@ Drop-in modules, each mirroring one reference interface:
 
 * :mod:`miattn.decode`  -- ``paged_decode``, ``paged_decode_plan``, ``PagedDecodePlan``,
   ``TRITON_AVAILABLE`` (reference ``model/triton_decode.py``);
-* :mod:`miattn.varlen`  -- ``HipVarlen`` / ``backend_for`` (reference
-  ``model/attention/varlen.py``, CUDA arm);
+* :mod:`miattn.varlen`  -- ``HipVarlen`` (also exported as ``FlashVarlen``), ``SdpaVarlen``,
+  ``backend_for`` (reference ``model/attention/varlen.py``);
 * :mod:`miattn.paged`   -- ``PagedPool``, ``PagedKV``, ``PagedWriteSink`` (reference
-  ``model/paged.py`` and ``serve/engine.py`` sinks);
-* :mod:`miattn.packed`  -- ``PackedPrefill`` (reference ``model/packed.py``);
-* :mod:`miattn.block_manager` -- ``BlockManager`` (reference ``serve/block_manager.py``).
+  ``model/paged.py`` and ``serve/engine.py``'s sink);
+* :mod:`miattn.packed`  -- ``PackedPrefill`` (reference ``model/packed.py``).
 
-All device work goes through ``libmiattn.so`` (C ABI in ``include/miattn.h``); when the
-library is missing the entry points raise instead of computing anything another way.
+Device work on a HIP device goes through ``libmiattn.so`` (C ABI in ``include/miattn.h``);
+when the library is missing those entry points raise instead of computing anything another
+way. Host (CPU) pools and the CPU prefill arm behave as the reference's own host arms.
 """
 
 from ._lib import HIP_AVAILABLE, LIB_PATH, LOAD_ERROR
-from .block_manager import BlockManager
 from .decode import TRITON_AVAILABLE, PagedDecodePlan, paged_decode, paged_decode_plan
 from .packed import PackedPrefill, as_packed_prefill
 from .paged import PagedKV, PagedPool, PagedWriteSink
-from .varlen import HipVarlen, backend_for
+from .varlen import FlashVarlen, HipVarlen, SdpaVarlen, backend_for
 
 __all__ = [
-    "HIP_AVAILABLE", "LIB_PATH", "LOAD_ERROR", "TRITON_AVAILABLE", "BlockManager", "PagedDecodePlan",
-    "paged_decode", "paged_decode_plan", "PackedPrefill", "as_packed_prefill", "PagedKV", "PagedPool",
-    "PagedWriteSink", "HipVarlen", "backend_for",
+    "HIP_AVAILABLE", "LIB_PATH", "LOAD_ERROR", "TRITON_AVAILABLE", "PagedDecodePlan", "paged_decode",
+    "paged_decode_plan", "PackedPrefill", "as_packed_prefill", "PagedKV", "PagedPool", "PagedWriteSink",
+    "FlashVarlen", "HipVarlen", "SdpaVarlen", "backend_for",
 ]

@@ -109,9 +109,9 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "mi_qk_norm_rope_write": (
         _c_int,
-        [_c_void_p, _c_int64, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int64, _c_void_p,
+        [_c_void_p, _c_int64, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int64, _c_int, _c_void_p,
          _c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
-         _c_int, _c_int64, _c_float, _c_int, _c_void_p, _c_void_p],
+         _c_int, _c_int64, _c_float, _c_int, _c_int, _c_void_p, _c_void_p],
     ),
     "mi_varlen_prefill": (
         _c_int,
@@ -121,7 +121,7 @@ SIGNATURES: dict[str, tuple] = {
     ),
 }
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 
 def _load():

@@ -1,322 +1,317 @@
 """Block-table paged decode on the HIP kernel: the drop-in for ``model/triton_decode.py``.
 
-Entry points keep the reference's names, signatures, ownership and error behaviour
-(reference ``model/triton_decode.py:250-538``):
+Public surface (names, signatures, ownership and exception split as in the reference,
+``model/triton_decode.py:250-258, 331-538``):
 
-* ``paged_decode(q, k_cache, v_cache, block_table, seqlen, *, scale=None) -> Tensor``
-  validates the full contract on every call, allocates a fresh ``out`` and never mutates
-  an input (reference ``:250-328``);
-* ``paged_decode_plan(...) -> PagedDecodePlan`` validates every layer's pools once;
-  ``PagedDecodePlan.run(layer, q)`` re-checks only the query layout (reference
-  ``:331-538``). The plan holds the pools, block table and seqlen by reference, so the
-  container's in-place seqlen updates are seen;
-* ``TRITON_AVAILABLE`` -- the availability flag callers import (reference
-  ``model/paged.py:58``, ``serve/engine.py:857-861``). It is True when the HIP library
-  loaded; the name is kept so callers switch over unchanged.
+* ``paged_decode(q, k_cache, v_cache, block_table, seqlen, *, scale=None) -> Tensor`` --
+  one query token per row against a paged pool. Checks the whole contract, returns a new
+  ``out`` and leaves every input untouched;
+* ``paged_decode_plan(q, k_caches, v_caches, block_table, seqlen, *, scale=None)`` ->
+  :class:`PagedDecodePlan`, whose ``run(layer, q)`` launches one layer. The plan checks all
+  layers once and afterwards only the query of each call; it keeps the pools, the table
+  and ``seqlen`` by reference, so in-place ``seqlen`` updates between steps are seen;
+* ``TRITON_AVAILABLE`` -- the flag the reference's callers import. It names the decode
+  backend being present, which here means ``libmiattn.so`` loaded.
 
-Contract (unchanged from the reference): ``q`` ``(B, H, D)``; ``k_cache``/``v_cache``
-``(n_blocks, block_size, H_kv, D)`` sharing q's dtype (fp32, fp16 or bf16);
-``block_table`` ``(B, max_blocks)`` int32 on q's device; ``seqlen`` ``(B,)`` int32 or int64
-with values in ``[0, max_blocks * block_size]``; ``scale=None`` means ``1/sqrt(D)``.
+Contract: ``q`` ``(B, H, D)``; pools ``(n_blocks, block_size, H_kv, D)`` in q's dtype
+(fp32, fp16 or bf16), ``H % H_kv == 0``, power-of-two ``block_size`` and ``D``;
+``block_table`` ``(B, width)`` int32; ``seqlen`` ``(B,)`` int32 or int64 within
+``[0, width * block_size]``; all on one HIP device. ``scale=None`` is ``1/sqrt(D)``.
 
-What differs underneath: the kernel is ``mi_paged_decode`` in ``libmiattn.so`` (one
-workgroup per (row, split, KV-head group) sweeping whole pages for every KV head and
-serving all GQA query heads; rows longer than one split are merged by a small
-log-sum-exp launch). Split-K needs a workspace;
-``paged_decode`` takes one from torch's caching allocator per call and a plan owns one for
-all its layers, so the runs of one plan must stay ordered on one stream (the decode layer
-loop is). The kernels also need the K/V
-pools' ``head_dim`` to be contiguous and 16-byte aligned, which every pool
-``PagedPool`` allocates is; any other layout raises ``ValueError``.
+Underneath is ``mi_paged_decode`` (``include/miattn.h``): page-sweeping split-K workgroups
+serving every query head of a KV head, plus a log-sum-exp merge launch for rows cut into
+several splits. The split partials live in a workspace: ``paged_decode`` takes one from
+torch's caching allocator per call; a plan owns one for all its layers, so one plan's runs
+must stay ordered on one stream (a layer loop is).
 """
 
 from __future__ import annotations
 
 import math
+from dataclasses import dataclass
+from types import SimpleNamespace
 
 import torch
 
 from . import _lib
+from ._contract import Rule, enforce, is_pow2
 
 __all__ = ["TRITON_AVAILABLE", "HIP_AVAILABLE", "paged_decode", "paged_decode_plan", "PagedDecodePlan"]
 
 HIP_AVAILABLE: bool = _lib.HIP_AVAILABLE
-#: Name kept from the reference so callers that gate on it switch over unchanged.
+#: Availability flag under the name the reference's callers import.
 TRITON_AVAILABLE: bool = HIP_AVAILABLE
 
-#: Last seqlen range validation: ``(seqlen, version, capacity)``; holding the tensor pins
-#: its storage so an identity match cannot alias a freed tensor (reference :92, :207-231).
-_SEQ_CHECK: tuple[torch.Tensor, int, int] | None = None
+_ELEMENT_TYPES = (torch.float16, torch.bfloat16, torch.float32)
+
+
+@dataclass(frozen=True)
+class DecodeGeometry:
+    """Sizes one decode launch is built from (all read from tensor shapes)."""
+
+    rows: int          # B
+    q_heads: int       # H
+    kv_heads: int      # H_kv
+    head_dim: int      # D
+    page: int          # block_size: tokens per physical block
+    width: int         # block-table columns
+
+    @property
+    def capacity(self) -> int:
+        return self.width * self.page
+
+    def dims(self) -> tuple[int, int, int, int, int, int]:
+        return (self.rows, self.q_heads, self.kv_heads, self.head_dim, self.page, self.width)
+
+
+# -- the contract, in the order a caller learns about mistakes ------------------------
+_LAYOUT = (
+    Rule(lambda a: a.q.dim() != 3, ValueError,
+         lambda a: f"q must be (B, H, D), got shape {tuple(a.q.shape)}"),
+    Rule(lambda a: a.k.dim() != 4 or a.v.dim() != 4, ValueError,
+         lambda a: "k_cache/v_cache must be (n_blocks, block_size, H_kv, D), got "
+                   f"{tuple(a.k.shape)} / {tuple(a.v.shape)}"),
+    Rule(lambda a: a.k.shape != a.v.shape, ValueError,
+         lambda a: f"k_cache/v_cache shapes differ: {tuple(a.k.shape)} vs {tuple(a.v.shape)}"),
+    Rule(lambda a: a.q.dtype not in _ELEMENT_TYPES, ValueError,
+         lambda a: f"q dtype must be fp16, bf16 or fp32, got {a.q.dtype}"),
+    Rule(lambda a: not (a.q.dtype == a.k.dtype == a.v.dtype), ValueError,
+         lambda a: f"q/k_cache/v_cache must share one dtype, got {a.q.dtype}, {a.k.dtype}, {a.v.dtype}"),
+)
+
+_HEADS = (
+    Rule(lambda a: a.q.shape[2] < 1, ValueError,
+         lambda a: f"head_dim must be positive, got {a.q.shape[2]}"),
+    Rule(lambda a: a.q.shape[2] != a.k.shape[3], ValueError,
+         lambda a: f"q head_dim {a.q.shape[2]} != cache head_dim {a.k.shape[3]}"),
+    Rule(lambda a: a.k.shape[2] < 1 or a.q.shape[1] % a.k.shape[2] != 0, ValueError,
+         lambda a: f"n_head ({a.q.shape[1]}) must be a multiple of n_kv_head ({a.k.shape[2]})"),
+    Rule(lambda a: not is_pow2(a.k.shape[1]), ValueError,
+         lambda a: "block_size must be a power of two (16 and 32 are the supported sizes), "
+                   f"got {a.k.shape[1]}"),
+    Rule(lambda a: not is_pow2(a.q.shape[2]), ValueError,
+         lambda a: f"head_dim must be a power of two for the kernel, got {a.q.shape[2]}"),
+)
+
+_INDEXING = (
+    Rule(lambda a: a.table.dim() != 2, ValueError,
+         lambda a: f"block_table must be (B, max_blocks), got shape {tuple(a.table.shape)}"),
+    Rule(lambda a: a.table.shape[0] != a.q.shape[0], ValueError,
+         lambda a: f"block_table batch {a.table.shape[0]} does not match q batch {a.q.shape[0]}"),
+    Rule(lambda a: a.table.dtype != torch.int32, ValueError,
+         lambda a: "paged_decode requires an int32 block_table (the kernel reads 32-bit block ids); "
+                   f"got {a.table.dtype}. Convert once where the tables are built."),
+    Rule(lambda a: a.seqlen.dim() != 1, ValueError,
+         lambda a: f"seqlen must be (B,), got shape {tuple(a.seqlen.shape)}"),
+    Rule(lambda a: a.seqlen.shape[0] != a.q.shape[0], ValueError,
+         lambda a: f"seqlen has {a.seqlen.shape[0]} entries for a batch of {a.q.shape[0]}"),
+    Rule(lambda a: a.seqlen.dtype not in (torch.int32, torch.int64), ValueError,
+         lambda a: f"seqlen must be int32 or int64, got {a.seqlen.dtype}"),
+    Rule(lambda a: any(t.device != a.q.device for t in (a.k, a.v, a.table, a.seqlen)), ValueError,
+         lambda a: "all paged_decode tensors must share one device; got q on "
+                   f"{a.q.device}, k_cache {a.k.device}, v_cache {a.v.device}, "
+                   f"block_table {a.table.device}, seqlen {a.seqlen.device}"),
+)
+
+# The HIP kernel streams each (token, KV head) row of D elements as 16-byte pieces.
+_POOL_LAYOUT = (
+    Rule(lambda a: a.k.stride(3) != 1 or a.v.stride(3) != 1, ValueError,
+         lambda a: "the HIP decode reads head_dim-contiguous pools; got strides "
+                   f"{a.k.stride()} / {a.v.stride()}"),
+    Rule(lambda a: (a.k.data_ptr() | a.v.data_ptr()) % 16 != 0, ValueError,
+         lambda a: "the HIP decode needs 16-byte aligned pools"),
+)
+
+
+class _SeqlenWatch:
+    """Range check of ``seqlen`` values, paid once per tensor version.
+
+    Reading ``seqlen`` costs a host synchronisation, so the last tensor that passed is
+    remembered with its version counter and the capacity it was checked against; the
+    same tensor at the same version skips the read. Inference-mode tensors carry no
+    version counter and are remembered under version -1, as the reference does
+    (``model/triton_decode.py:207-231``). Keeping the tensor object alive in the watch is
+    what makes the identity comparison safe.
+    """
+
+    __slots__ = ("_seen",)
+
+    def __init__(self) -> None:
+        self._seen: tuple[torch.Tensor, int, int] | None = None
+
+    def confirm(self, seqlen: torch.Tensor, capacity: int) -> None:
+        version = -1 if seqlen.is_inference() else int(seqlen._version)
+        seen = self._seen
+        if seen is not None and seen[0] is seqlen and seen[1] == version and seen[2] == capacity:
+            return
+        lo, hi = (int(x) for x in torch.stack(torch.aminmax(seqlen)).tolist())
+        if lo < 0:
+            raise ValueError(f"seqlen values must be >= 0, got {lo}")
+        if hi > capacity:
+            raise ValueError(f"seqlen {hi} exceeds the block table capacity {capacity}")
+        self._seen = (seqlen, version, capacity)
+
+
+_SEQLEN_WATCH = _SeqlenWatch()
 
 
 def _require_backend() -> None:
-    """Fail loudly: there is no eager or CPU implementation behind this entry point."""
+    """No library or no device is an environment failure, never a reason to compute
+    the attention some other way."""
     if not TRITON_AVAILABLE:
         raise RuntimeError(
-            "paged_decode requires the HIP kernel library libmiattn.so (the replacement of "
-            "the Triton decode kernel), but it is unavailable: "
-            f"{_lib.LOAD_ERROR or 'disabled'}. There is no eager fallback; the dense "
-            "numeric oracle lives in oracle/."
+            "paged_decode needs libmiattn.so, the HIP kernel that stands in for the Triton "
+            f"decode kernel, and it is not loaded ({_lib.LOAD_ERROR or 'disabled'}); "
+            "there is no eager implementation to use instead"
         )
     if not torch.cuda.is_available():
         raise RuntimeError(
-            "paged_decode requires CUDA (a HIP device), but torch.cuda is unavailable; the "
-            "paged decode arm has no CPU fallback. The dense numeric oracle lives in oracle/."
+            "paged_decode runs on a CUDA (HIP) device and torch reports none; "
+            "the paged arm has no host implementation"
         )
 
 
-def _require_cuda_tensors(tensors) -> None:
-    for name, tensor in tensors:
+def _require_device_tensors(named) -> None:
+    for name, tensor in named:
         if not tensor.is_cuda:
             raise RuntimeError(
-                f"paged_decode requires CUDA tensors, got {name} on device {tensor.device}; "
-                "there is no silent fallback to a dense implementation."
+                f"paged_decode requires CUDA tensors; {name} is on {tensor.device} and "
+                "nothing here computes on the host"
             )
 
 
-def _validate(q, k_cache, v_cache, block_table, seqlen) -> None:
-    """The reference's layout contract (reference :120-231): structural errors are
-    ``ValueError``; the seqlen range check is cached per tensor version."""
-    if q.dim() != 3:
-        raise ValueError(f"q must be (B, H, D), got shape {tuple(q.shape)}")
-    if k_cache.dim() != 4 or v_cache.dim() != 4:
-        raise ValueError(
-            "k_cache/v_cache must be (n_blocks, block_size, H_kv, D), got "
-            f"{tuple(k_cache.shape)} / {tuple(v_cache.shape)}"
-        )
-    if tuple(k_cache.shape) != tuple(v_cache.shape):
-        raise ValueError(
-            f"k_cache/v_cache shapes differ: {tuple(k_cache.shape)} vs {tuple(v_cache.shape)}"
-        )
-    if q.dtype not in (torch.float16, torch.bfloat16, torch.float32):
-        raise ValueError(f"q dtype must be fp16, bf16 or fp32, got {q.dtype}")
-    if not (k_cache.dtype == v_cache.dtype == q.dtype):
-        raise ValueError(
-            "q/k_cache/v_cache must share one dtype, got "
-            f"{q.dtype}, {k_cache.dtype}, {v_cache.dtype}"
-        )
-    B, H, D = q.shape
-    _, block_size, H_kv, cache_d = k_cache.shape
-    if D < 1:
-        raise ValueError(f"head_dim must be positive, got {D}")
-    if D != cache_d:
-        raise ValueError(f"q head_dim {D} != cache head_dim {cache_d}")
-    if H_kv < 1 or H % H_kv != 0:
-        raise ValueError(f"n_head ({H}) must be a multiple of n_kv_head ({H_kv})")
-    if block_size < 1:
-        raise ValueError(f"block_size must be positive, got {block_size}")
-    if block_size & (block_size - 1):
-        raise ValueError(
-            f"block_size must be a power of two (16 and 32 are the supported sizes), got {block_size}"
-        )
-    if D & (D - 1):
-        raise ValueError(f"head_dim must be a power of two for the kernel, got {D}")
-    if block_table.dim() != 2:
-        raise ValueError(
-            f"block_table must be (B, max_blocks), got shape {tuple(block_table.shape)}"
-        )
-    B_bt, max_blocks = block_table.shape
-    if B_bt != B:
-        raise ValueError(f"block_table batch {B_bt} does not match q batch {B}")
-    if block_table.dtype != torch.int32:
-        raise ValueError(
-            "paged_decode requires an int32 block_table (the kernel's indexing contract); "
-            f"got {block_table.dtype}. Cast at the allocator boundary, not per step."
-        )
-    if seqlen.dim() != 1:
-        raise ValueError(f"seqlen must be (B,), got shape {tuple(seqlen.shape)}")
-    if seqlen.shape[0] != B:
-        raise ValueError(f"seqlen has {seqlen.shape[0]} entries for a batch of {B}")
-    if seqlen.dtype not in (torch.int32, torch.int64):
-        raise ValueError(f"seqlen must be int32 or int64, got {seqlen.dtype}")
-    for name, tensor in (
-        ("q", q), ("k_cache", k_cache), ("v_cache", v_cache),
-        ("block_table", block_table), ("seqlen", seqlen),
-    ):
-        if tensor.device != q.device:
-            raise ValueError(
-                f"{name} is on {tensor.device} but q is on {q.device}; all paged_decode "
-                "tensors must share one device"
-            )
-    if B == 0:
-        return
-    capacity = max_blocks * block_size
-    global _SEQ_CHECK
-    version = -1 if seqlen.is_inference() else int(seqlen._version)
-    cached = _SEQ_CHECK
-    if cached is not None and cached[0] is seqlen and cached[1] == version and cached[2] == capacity:
-        return
-    low = int(seqlen.min())
-    high = int(seqlen.max())
-    if low < 0:
-        raise ValueError(f"seqlen values must be >= 0, got {low}")
-    if high > capacity:
-        raise ValueError(
-            f"seqlen {high} exceeds the block table capacity {capacity} "
-            f"({max_blocks} blocks x {block_size} tokens)"
-        )
-    _SEQ_CHECK = (seqlen, version, capacity)
+def _check(q, k_cache, v_cache, block_table, seqlen) -> DecodeGeometry:
+    """Apply the full contract and return the launch geometry."""
+    a = SimpleNamespace(q=q, k=k_cache, v=v_cache, table=block_table, seqlen=seqlen)
+    enforce(_LAYOUT, a)
+    enforce(_HEADS, a)
+    enforce(_INDEXING, a)
+    g = DecodeGeometry(int(q.shape[0]), int(q.shape[1]), int(k_cache.shape[2]), int(q.shape[2]),
+                       int(k_cache.shape[1]), int(block_table.shape[1]))
+    if g.rows:
+        _SEQLEN_WATCH.confirm(seqlen, g.capacity)
+    return g
 
 
-def _workspace(q, H: int, H_kv: int, D: int, block_size: int, max_blocks: int) -> torch.Tensor | None:
-    """Split-K partials buffer, sized exactly for this shape and dtype (None if unneeded)."""
-    n = int(_lib.lib.mi_paged_decode_workspace_size(q.shape[0], H, H_kv, D, block_size, max_blocks,
-                                                     _lib.dtype_code(q.dtype)))
-    if n == 0:
-        return None
-    return torch.empty(n, dtype=torch.uint8, device=q.device)
+def _workspace_bytes(g: DecodeGeometry, dtype: torch.dtype) -> int:
+    return int(_lib.lib.mi_paged_decode_workspace_size(*g.dims(), _lib.dtype_code(dtype)))
 
 
-def _strides(q, k_cache, v_cache, out, block_table) -> list[int]:
-    return [*q.stride(), *k_cache.stride(), *v_cache.stride(), *out.stride(), block_table.stride(0)]
+def _launch(g: DecodeGeometry, q, k_ptr: int, v_ptr: int, table_ptr: int, seqlen_ptr: int, out,
+            strides, scale: float, ws_ptr, ws_bytes: int, what: str) -> None:
+    rc = _lib.lib.mi_paged_decode(
+        q.data_ptr(), k_ptr, v_ptr, table_ptr, seqlen_ptr, out.data_ptr(), *g.dims(), strides,
+        scale, _lib.dtype_code(q.dtype), ws_ptr, ws_bytes, _lib.current_stream(q.device),
+    )
+    _lib.check(rc, what)
 
 
 def paged_decode(q, k_cache, v_cache, block_table, seqlen, *, scale: float | None = None):
-    """Decode one query token per row against a paged KV pool (reference :250-328)."""
+    """Decode one query token per row against a paged KV pool (reference
+    ``model/triton_decode.py:250-328``)."""
     _require_backend()
-    _require_cuda_tensors(
-        (("q", q), ("k_cache", k_cache), ("v_cache", v_cache),
-         ("block_table", block_table), ("seqlen", seqlen))
-    )
-    _validate(q, k_cache, v_cache, block_table, seqlen)
-    B, H, D = q.shape
-    _, block_size, H_kv, _ = k_cache.shape
-    if B == 0:
+    _require_device_tensors((("q", q), ("k_cache", k_cache), ("v_cache", v_cache),
+                             ("block_table", block_table), ("seqlen", seqlen)))
+    g = _check(q, k_cache, v_cache, block_table, seqlen)
+    if g.rows == 0:
         return torch.empty_like(q)
+    enforce(_POOL_LAYOUT, SimpleNamespace(k=k_cache, v=v_cache))
     q = q.contiguous()
-    if block_table.stride(1) != 1:
-        block_table = block_table.contiguous()
-    seqlen = seqlen.contiguous()
-    seqlen32 = seqlen if seqlen.dtype == torch.int32 else seqlen.to(torch.int32)
+    table = block_table if block_table.stride(1) == 1 else block_table.contiguous()
+    lens = seqlen.to(torch.int32).contiguous()
     out = torch.empty_like(q)
-    if scale is None:
-        scale = 1.0 / math.sqrt(D)
-    max_blocks = block_table.shape[1]
-    ws = _workspace(q, H, H_kv, D, block_size, max_blocks)
-    rc = _lib.lib.mi_paged_decode(
-        q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), block_table.data_ptr(),
-        seqlen32.data_ptr(), out.data_ptr(), B, H, H_kv, D, block_size, max_blocks,
-        _lib.int64_array(_strides(q, k_cache, v_cache, out, block_table)), float(scale),
-        _lib.dtype_code(q.dtype), ws.data_ptr() if ws is not None else None,
-        ws.numel() if ws is not None else 0, _lib.current_stream(q.device),
-    )
-    _lib.check(rc, "paged_decode")
+    strides = _lib.int64_array((*q.stride(), *k_cache.stride(), *v_cache.stride(), *out.stride(),
+                                table.stride(0)))
+    n_ws = _workspace_bytes(g, q.dtype)
+    ws = torch.empty(n_ws, dtype=torch.uint8, device=q.device) if n_ws else None
+    _launch(g, q, k_cache.data_ptr(), v_cache.data_ptr(), table.data_ptr(), lens.data_ptr(), out, strides,
+            float(1.0 / math.sqrt(g.head_dim) if scale is None else scale),
+            None if ws is None else ws.data_ptr(), n_ws, "paged_decode")
     return out
 
 
-class PagedDecodePlan:
-    """Per-container launch metadata for repeated decode calls (reference :331-520).
+# -- launch plan ------------------------------------------------------------------------
+_PLAN_INPUTS = (
+    Rule(lambda a: a.q.dim() != 3, ValueError,
+         lambda a: f"q must be (B, H, D), got shape {tuple(a.q.shape)}"),
+    Rule(lambda a: not a.q.is_contiguous(), ValueError,
+         lambda a: f"paged_decode_plan needs a contiguous (B, H, D) query, got strides {a.q.stride()}"),
+    Rule(lambda a: a.q.shape[0] == 0, ValueError,
+         lambda a: "paged_decode_plan needs at least one row"),
+    Rule(lambda a: a.seqlen.dtype != torch.int32, ValueError,
+         lambda a: "paged_decode_plan requires an int32 seqlen: the plan reads the caller's tensor "
+                   f"in place at every run, so it cannot keep a converted copy (got {a.seqlen.dtype})"),
+    Rule(lambda a: a.seqlen.dim() != 1 or a.seqlen.stride(0) != 1, ValueError,
+         lambda a: f"paged_decode_plan requires a contiguous 1-D seqlen, got strides {a.seqlen.stride()}"),
+    Rule(lambda a: a.table.dim() != 2 or a.table.stride(1) != 1, ValueError,
+         lambda a: "paged_decode_plan requires a column-contiguous block table, got strides "
+                   f"{a.table.stride()}"),
+    Rule(lambda a: len(a.ks) == 0 or len(a.ks) != len(a.vs), ValueError,
+         lambda a: f"paged_decode_plan needs one k_cache and one v_cache per layer, got {len(a.ks)} / {len(a.vs)}"),
+)
 
-    Validates every ``(k_cache, v_cache)`` pair once (the full ``paged_decode`` contract
-    including the seqlen range check) and prebuilds the C-ABI argument block; ``run``
-    re-checks only the query, the one input that changes per layer. Pools, block table
-    and seqlen are held by reference: in-place seqlen/table updates are seen, replacing a
-    pool tensor requires a new plan. The plan owns the split-K workspace shared by its
-    layers, so its runs must be ordered on one stream.
+
+class PagedDecodePlan:
+    """Checked-once launch state for the decode calls of one container (reference
+    ``model/triton_decode.py:331-520``).
+
+    Construction applies the full :func:`paged_decode` contract to every layer's pools
+    and requires them to share one shape and one stride layout; it then freezes the
+    launch arguments (geometry, stride block, scale, workspace). ``run`` only compares
+    the query against the layout it was built for. Pools, table and ``seqlen`` are held
+    by reference.
     """
 
-    __slots__ = (
-        "n_layer", "q_shape", "q_dtype", "q_device", "q_strides", "_k", "_v",
-        "_block_table", "_seqlen", "_scale", "_dims", "_strides", "_ws", "_ws_bytes", "_dtype",
-    )
+    __slots__ = ("n_layer", "geometry", "q_signature", "_k_ptrs", "_v_ptrs", "_pools",
+                 "_table", "_seqlen", "_strides", "_scale", "_ws", "_ws_bytes")
 
     def __init__(self, q, k_caches, v_caches, block_table, seqlen, *, scale=None) -> None:
         _require_backend()
-        _require_cuda_tensors((("q", q), ("block_table", block_table), ("seqlen", seqlen)))
-        if q.dim() != 3:
-            raise ValueError(f"q must be (B, H, D), got shape {tuple(q.shape)}")
-        if not q.is_contiguous():
-            raise ValueError(
-                "paged_decode_plan needs a contiguous (B, H, D) query, got strides "
-                f"{q.stride()}; call .contiguous() once, not per layer"
-            )
-        b, h, d = q.shape
-        if b == 0:
-            raise ValueError("paged_decode_plan needs at least one row")
-        if seqlen.dtype != torch.int32:
-            raise ValueError(
-                "paged_decode_plan requires an int32 seqlen so in-place updates are "
-                f"visible; got {seqlen.dtype}. Cast once at the container boundary."
-            )
-        if seqlen.stride(0) != 1:
-            raise ValueError(
-                f"paged_decode_plan requires a contiguous 1-D seqlen; got strides {seqlen.stride()}"
-            )
-        if block_table.stride(1) != 1:
-            raise ValueError(
-                "paged_decode_plan requires a column-contiguous block table; got strides "
-                f"{block_table.stride()}"
-            )
-        k_caches = list(k_caches)
-        v_caches = list(v_caches)
-        if len(k_caches) != len(v_caches) or not k_caches:
-            raise ValueError(
-                "paged_decode_plan needs one k_cache/v_cache per layer, got "
-                f"{len(k_caches)} / {len(v_caches)}"
-            )
-        for layer, (k_cache, v_cache) in enumerate(zip(k_caches, v_caches)):
-            _require_cuda_tensors(((f"k_cache[{layer}]", k_cache), (f"v_cache[{layer}]", v_cache)))
-            _validate(q, k_cache, v_cache, block_table, seqlen)
-            if tuple(k_cache.shape) != tuple(k_caches[0].shape) or tuple(v_cache.shape) != tuple(
-                v_caches[0].shape
-            ):
-                raise ValueError("paged_decode_plan needs one pool shape for every layer")
-            if k_cache.stride() != k_caches[0].stride():
-                raise ValueError("paged_decode_plan needs one pool layout for every layer")
-            if v_cache.stride() != v_caches[0].stride():
-                raise ValueError("paged_decode_plan needs one v-pool layout for every layer")
-        self.n_layer = len(k_caches)
-        self._k = k_caches
-        self._v = v_caches
-        self._block_table = block_table
+        _require_device_tensors((("q", q), ("block_table", block_table), ("seqlen", seqlen)))
+        ks, vs = list(k_caches), list(v_caches)
+        enforce(_PLAN_INPUTS, SimpleNamespace(q=q, ks=ks, vs=vs, table=block_table, seqlen=seqlen))
+        first = (tuple(ks[0].shape), ks[0].stride(), vs[0].stride())
+        for layer, (k, v) in enumerate(zip(ks, vs)):
+            _require_device_tensors(((f"k_cache[{layer}]", k), (f"v_cache[{layer}]", v)))
+            g = _check(q, k, v, block_table, seqlen)
+            enforce(_POOL_LAYOUT, SimpleNamespace(k=k, v=v))
+            if (tuple(k.shape), k.stride(), v.stride()) != first or tuple(v.shape) != first[0]:
+                raise ValueError(f"paged_decode_plan needs one pool shape and layout for every layer "
+                                 f"(layer {layer} differs from layer 0)")
+        self.n_layer = len(ks)
+        self.geometry = g
+        self.q_signature = (tuple(q.shape), q.dtype, q.device, q.stride())
+        self._pools = (ks, vs)  # keeps the pool tensors alive
+        self._k_ptrs = [k.data_ptr() for k in ks]
+        self._v_ptrs = [v.data_ptr() for v in vs]
+        self._table = block_table
         self._seqlen = seqlen
-        self.q_shape = (int(b), int(h), int(d))
-        self.q_dtype = q.dtype
-        self.q_device = q.device
-        self.q_strides = (int(q.stride(0)), int(q.stride(1)), int(q.stride(2)))
-        self._scale = float(1.0 / math.sqrt(d) if scale is None else scale)
-        _, block_size, h_kv, _ = k_caches[0].shape
-        max_blocks = int(block_table.shape[1])
-        self._dims = (int(b), int(h), int(h_kv), int(d), int(block_size), max_blocks)
-        # q and out share the validated contiguous (B, H, D) strides; every layer's pool
-        # shares one stride tuple, so the 15-entry stride block is fixed for the plan.
-        self._strides = _lib.int64_array(
-            [*self.q_strides, *k_caches[0].stride(), *v_caches[0].stride(), *self.q_strides,
-             block_table.stride(0)]
-        )
-        self._ws = _workspace(q, int(h), int(h_kv), int(d), int(block_size), max_blocks)
-        self._ws_bytes = 0 if self._ws is None else int(self._ws.numel())
-        self._dtype = _lib.dtype_code(q.dtype)
+        # q and out share the checked contiguous (B, H, D) strides
+        self._strides = _lib.int64_array((*q.stride(), *first[1], *first[2], *q.stride(), block_table.stride(0)))
+        self._scale = float(1.0 / math.sqrt(g.head_dim) if scale is None else scale)
+        self._ws_bytes = _workspace_bytes(g, q.dtype)
+        self._ws = torch.empty(self._ws_bytes, dtype=torch.uint8, device=q.device) if self._ws_bytes else None
 
     def run(self, layer: int, q):
-        """Launch the kernel for one layer; ``q`` must match the validated layout."""
+        """Launch one layer; ``q`` must have the layout the plan was built with."""
         if not 0 <= int(layer) < self.n_layer:
-            raise IndexError(f"layer {layer} outside the plan's {self.n_layer} layers")
-        if (
-            tuple(q.shape) != self.q_shape
-            or q.dtype != self.q_dtype
-            or q.device != self.q_device
-            or q.stride() != self.q_strides
-        ):
+            raise IndexError(f"layer {layer} is outside the plan's {self.n_layer} layers")
+        signature = (tuple(q.shape), q.dtype, q.device, q.stride())
+        if signature != self.q_signature:
             raise ValueError(
-                "paged_decode_plan.run got a query that does not match the validated "
-                f"layout {(self.q_shape, self.q_dtype, self.q_strides)}; got "
-                f"{(tuple(q.shape), q.dtype, q.stride())}. Rebuild the plan for a new layout."
+                "paged_decode_plan.run: the query does not match the validated layout "
+                f"(built for shape/dtype/device/strides {self.q_signature}, got {signature}); "
+                "build a new plan for a new layout"
             )
         out = torch.empty_like(q)
-        b, h, h_kv, d, bs, mb = self._dims
-        rc = _lib.lib.mi_paged_decode(
-            q.data_ptr(), self._k[layer].data_ptr(), self._v[layer].data_ptr(),
-            self._block_table.data_ptr(), self._seqlen.data_ptr(), out.data_ptr(),
-            b, h, h_kv, d, bs, mb, self._strides, self._scale, self._dtype,
-            None if self._ws is None else self._ws.data_ptr(), self._ws_bytes,
-            _lib.current_stream(self.q_device),
-        )
-        _lib.check(rc, "paged_decode_plan.run")
+        layer = int(layer)
+        _launch(self.geometry, q, self._k_ptrs[layer], self._v_ptrs[layer], self._table.data_ptr(),
+                self._seqlen.data_ptr(), out, self._strides, self._scale,
+                None if self._ws is None else self._ws.data_ptr(), self._ws_bytes, "paged_decode_plan.run")
         return out
 
 
 def paged_decode_plan(q, k_caches, v_caches, block_table, seqlen, *, scale=None) -> PagedDecodePlan:
-    """Validate one container's decode tensors once and cache their launch metadata
-    (reference :523-538)."""
+    """Check one container's decode tensors once and freeze their launch arguments
+    (reference ``model/triton_decode.py:523-538``)."""
     return PagedDecodePlan(q, k_caches, v_caches, block_table, seqlen, scale=scale)

@@ -350,7 +350,9 @@ class GraphDecoder:
         for t, n in zip(tables, lengths):
             if (n + max_new + pool.block_size - 1) // pool.block_size > len(t):
                 raise ValueError(f"block table of {len(t)} blocks cannot hold {n} + {max_new} tokens")
-        bt = torch.zeros(B, max_blocks, dtype=torch.int32)
+        # rows padded with -1 past their own blocks: the step-begin launch refuses a row whose
+        # position reaches the padding instead of writing into another row's block
+        bt = torch.full((B, max_blocks), -1, dtype=torch.int32)
         for r, t in enumerate(tables):
             bt[r, : len(t)] = torch.tensor(t, dtype=torch.int32)
         self.table = bt.to(dev)
@@ -418,8 +420,14 @@ class GraphDecoder:
 
     def check(self) -> None:
         """Raise ``IndexError`` if a step met a token outside the vocabulary or a position
-        outside its row's block table (that row was skipped); one host synchronisation."""
+        outside its row's own blocks (that row was made inert: no K/V written, zero
+        attention), or if a write of the step was refused by the pool; host reads only."""
         bad = int(self.error.item())
         if bad:
             self.error.zero_()
+            try:
+                self.pool.check_writes()  # the refused row's epilogue writes were skipped too
+            except IndexError:
+                pass
             raise IndexError(f"row {bad - 1}: token or position out of range in a decode step; the row was skipped")
+        self.pool.check_writes()

@@ -44,10 +44,10 @@ def test_error_channel_reports_the_last_failure():
         _lib.check(rc, "probe")
 
 
-KERNELS = {"staged": 0, "ring": 1, "wide": 2, "duo": 3}
-ROWS = {0: 64, 1: 128, 2: 64, 3: 64}   # query rows per tile
-KEYS = {0: 64, 1: 64, 2: 128, 3: 64}   # keys per unit of a tile's work
-PER_CU = {0: 2, 1: 1, 2: 1, 3: 2}      # workgroups one CU runs at once
+KERNELS = {"staged": 0, "ring": 1, "duo": 3}
+ROWS = {0: 64, 1: 128, 3: 64}   # query rows per tile
+KEYS = {0: 64, 1: 64, 3: 64}    # keys per unit of a tile's work
+PER_CU = {0: 2, 1: 1, 3: 2}     # workgroups one CU runs at once
 
 
 def _kind(kernel, D, lengths=()):
@@ -143,11 +143,10 @@ def _piece_work(lengths, p, kind):
 @pytest.mark.parametrize("lengths,H,kernel", [
     ([100, 1, 700, 64, 65, 1742, 450], 16, None),     # duo kernel (< 8192 tokens), fills the chip
     ([100, 1, 700, 64, 65, 1742, 450], 16, "staged"),
-    ([100, 1, 700, 64, 65, 1742, 450], 16, "wide"),   # fills the chip: not split
     ([100, 1, 2100, 64, 65], 4, "ring"),              # underfilled: split pieces
     ([100, 8200], 2, None),                           # ring kernel (>= 8192 tokens), underfilled
     ([100, 1, 2100, 64, 65], 4, None),                # duo kernel, underfilled: split pieces
-    ([100, 1, 2100, 64, 65], 2, "wide"),
+    ([100, 1, 2100, 64, 65], 2, "ring"),
     ([100, 1, 2100, 64, 65], 4, "duo"),
 ])
 def test_schedule_covers_every_tile_once_heaviest_first(lengths, H, kernel):
@@ -177,11 +176,11 @@ def test_schedule_covers_every_tile_once_heaviest_first(lengths, H, kernel):
     assert n_work == len(pieces)
 
 
-@pytest.mark.parametrize("kernel,H", [("ring", 8), ("wide", 4), ("duo", 8)])
+@pytest.mark.parametrize("kernel,H", [("ring", 8), ("ring", 4), ("duo", 8)])
 def test_schedule_splits_only_launches_that_underfill_the_chip(kernel, H):
     kind = KERNELS[kernel]
     rows = ROWS[kind]
-    # one 2100-token segment: 17 ring tiles x 8 heads or 33 wide tiles x 4 heads < 256 CUs,
+    # one 2100-token segment: 17 ring tiles x 8 or 4 heads, 33 duo tiles x 8 heads < the chip,
     # so long tiles are cut to the per-CU share of the work (at least 8 units, at most 4
     # pieces)
     lengths = [2100]
@@ -210,7 +209,8 @@ def test_schedule_rejects_unknown_kernels_and_head_dims():
     host_cu = (ctypes.c_int32 * 2)(0, 5)
     assert _lib.lib.mi_varlen_schedule_for(host_cu, 1, 16, 8, 128, 1, 7, None, 0) == _lib.MI_ERR_INVALID
     assert _lib.lib.mi_varlen_schedule_for(host_cu, 1, 16, 8, 128, 1, -2, None, 0) == _lib.MI_ERR_INVALID
-    assert _lib.lib.mi_varlen_schedule_for(host_cu, 1, 16, 8, 256, 1, 2, None, 0) == _lib.MI_ERR_UNSUPPORTED
+    assert _lib.lib.mi_varlen_schedule_for(host_cu, 1, 16, 8, 128, 1, 2, None, 0) == _lib.MI_ERR_INVALID  # removed
+    assert _lib.lib.mi_varlen_schedule_for(host_cu, 1, 16, 8, 256, 1, 1, None, 0) == _lib.MI_ERR_UNSUPPORTED
     assert _lib.lib.mi_varlen_schedule_for(host_cu, 1, 16, 8, 256, 1, 0, None, 0) > 0
 
 

@@ -266,3 +266,57 @@ def test_config4_long_context_split_k(cuda):
     v2[perm] = inp.v_caches[0]
     table2 = perm[inp.block_table.long()].to(torch.int32)
     assert torch.equal(paged_decode(inp.q[0], k2, v2, table2, inp.seqlen), got)
+
+
+def test_config4_full_size_one_layer(cuda):
+    """Config 4 at its real size: B=32 rows x 8192 tokens, 16384 permuted blocks, a 512-wide
+    table (16 splits per row, one merge round), against the fp32 gather oracle, through
+    both entry points (the plan is what bench.py times)."""
+    inp = W.paged_decode_config(B=32, lengths=[8192] * 32, n_blocks=16384, n_layer=1, device=cuda,
+                                max_blocks=512, seed=4)
+    got = paged_decode(inp.q[0], inp.k_caches[0], inp.v_caches[0], inp.block_table, inp.seqlen)
+    plan = paged_decode_plan(inp.q[0], inp.k_caches, inp.v_caches, inp.block_table, inp.seqlen)
+    assert torch.equal(plan.run(0, inp.q[0]), got)
+    expected = reference_paged_decode(inp.q[0].cpu(), inp.k_caches[0].cpu(), inp.v_caches[0].cpu(),
+                                      inp.block_table.cpu(), inp.seqlen.cpu(), out_dtype=torch.float32)
+    got = got.cpu().float()
+    assert (got - expected).abs().max() <= 2e-2
+    excess = ((got - expected).abs() - expected.abs() * 2.0 ** -8).max().item()
+    assert excess <= 1e-3, f"error beyond bf16 rounding {excess}"
+
+
+@pytest.mark.parametrize("dtype,D", [(torch.float32, 64), (torch.bfloat16, 128)], ids=["fp32-d64", "bf16-d128"])
+def test_duplicated_blocks_and_an_unread_table_tail(dtype, D, cuda):
+    """The reference's odd tables on the HIP kernel (reference
+    tests/unit/test_triton_decode.py:147-169): row 0 reads physical block 3 as its pages 0
+    and 2, the last page's tail past seqlen 50 is dropped, and the table ends in -999
+    entries the kernel must never dereference (it walks only ceil(seqlen / 16) pages)."""
+    q, k, v, _, _ = _build(2, 4, 2, D, 16, [50, 64], dtype=dtype, seed=7, n_blocks=6, device="cpu")
+    table = torch.tensor([[3, 0, 3, 5, -999, -999], [5, 1, 4, 0, -999, -999]], dtype=torch.int32)
+    seqlen = torch.tensor([50, 64], dtype=torch.int32)
+    got = paged_decode(q.to(cuda), k.to(cuda), v.to(cuda), table.to(cuda), seqlen.to(cuda)).cpu()
+    expected = dense_decode_f64(q.double(), k.double(), v.double(), table, seqlen)
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    assert (got.double() - expected).abs().max().item() < tol
+    # the same tables inside a long row: pages beyond a 3000-token row are -999, ids repeat
+    gen = torch.Generator().manual_seed(8)
+    n_pages = (3000 + 15) // 16
+    table = torch.full((2, n_pages + 7), -999, dtype=torch.int32)
+    table[0, :n_pages] = torch.randint(0, 6, (n_pages,), generator=gen, dtype=torch.int32)
+    table[1, :4] = torch.tensor([5, 1, 4, 0])
+    seqlen = torch.tensor([3000, 64], dtype=torch.int32)
+    got = paged_decode(q.to(cuda), k.to(cuda), v.to(cuda), table.to(cuda), seqlen.to(cuda)).cpu()
+    expected = reference_paged_decode(q, k, v, table.clamp(min=0), seqlen, out_dtype=torch.float32)
+    assert (got.float() - expected).abs().max().item() < tol
+
+
+def test_zero_length_rows_next_to_long_rows(cuda):
+    """Rows of length 0 (exact zeros, reference :352-365) between split-K rows."""
+    lengths = [0, 5000, 0, 1, 3000, 0]
+    q, k, v, table, seqlen = _build(6, 16, 8, 128, 16, lengths, dtype=torch.bfloat16, seed=5)
+    got = paged_decode(q, k, v, table, seqlen).cpu()
+    for r, n in enumerate(lengths):
+        if n == 0:
+            assert not got[r].any()
+    expected = reference_paged_decode(*_cpu(q, k, v, table, seqlen), out_dtype=torch.float32)
+    assert (got.float() - expected).abs().max().item() <= 2e-2

@@ -126,3 +126,39 @@ def test_graph_replayed_decode_equals_eager_decode(model):
     eager = _free_run(model, use_graph=False)
     graph = _free_run(model, use_graph=True)
     assert torch.equal(eager, graph)
+
+
+def test_graph_step_past_one_rows_blocks_touches_no_other_row(model):
+    """A captured step replayed past one row's own blocks (GraphDecoder pads every row's
+    table with -1): that row is refused by the step-begin launch and made inert (slot -1,
+    seqlen 0), so no other row's blocks and none of the refused row's earlier K/V change,
+    and check() reports it."""
+    lengths = [40, 90]
+    tables, n_blocks = _tables(lengths, 8)      # row 0: 3 blocks (48 slots), row 1: 7 blocks
+    pool, logits = _prefill_lengths(model, lengths, tables, n_blocks)
+    dec = GraphDecoder(model, pool, tables, lengths, logits.argmax(-1), 8)
+    dec.capture()
+    for _ in range(8):                          # row 0 reaches position 47, its last slot
+        dec.step()
+    torch.cuda.synchronize()
+    dec.check()
+    before_k = [t.clone() for t in pool.keys]
+    before_v = [t.clone() for t in pool.values]
+    dec.step()                                  # row 0 at position 48: past its table
+    torch.cuda.synchronize()
+    with pytest.raises(IndexError, match="row 0"):
+        dec.check()
+    own = set(tables[0])
+    for layer in range(model.cfg.n_layer):
+        changed = ((pool.keys[layer] != before_k[layer]).flatten(1).any(1)
+                   | (pool.values[layer] != before_v[layer]).flatten(1).any(1)).nonzero().flatten().tolist()
+        # only row 1's block for position 98 may change; none of row 0's blocks, no other block
+        assert set(changed) <= {tables[1][98 // BS]}, f"layer {layer}: blocks {changed} changed"
+        assert not own & set(changed)
+
+
+def _prefill_lengths(model, lengths, tables, n_blocks):
+    gen = torch.Generator().manual_seed(5)
+    prompts = [torch.randint(0, model.cfg.vocab, (n,), generator=gen).tolist() for n in lengths]
+    pool = model.new_pool(n_blocks, BS)
+    return pool, model.prefill(prompts, pool, tables)

@@ -130,7 +130,7 @@ def test_packed_prefill_epilogue_matches_the_tensor_ops():
     packed = PackedPrefill(cu_seqlens=cu, positions=positions,
                            sinks=[PagedWriteSink(pools[0], t, n) for t, n in zip(tables, lengths)])
     q, k, v = packed.write_rope(0, qkv, qn, kn, cos, sin, eps)
-    slots = packed._packed_slots[1]
+    slots = packed.group_slots
     q_ref = _reference(pools[1], 0, qkv, qn, kn, cos, sin, positions, slots, H, H_kv, D, eps)
     torch.cuda.synchronize()
     assert q.shape == (1, T, H, D) and k.shape == (1, T, H_kv, D) and v.shape == (1, T, H_kv, D)
@@ -187,3 +187,56 @@ def test_decode_step_ops_reject_bad_shapes():
         add_rms_norm(x, x[:, :4].contiguous(), torch.ones(8, dtype=torch.bfloat16, device="cuda"), 1e-6)
     with pytest.raises(ValueError, match="gate_up"):
         silu_mul(torch.zeros(4, 7, dtype=torch.bfloat16, device="cuda"))
+
+
+def _qwen35_norm(x, w, eps):
+    """Qwen3.5's zero-centred q/k norm (reference model/qwen35.py:83-89): fp32 throughout,
+    ``x * rsqrt(mean(x^2) + eps) * (1 + w)``, cast back once."""
+    xf = x.float()
+    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * (1.0 + w.float())).to(x.dtype)
+
+
+def _partial_rope(x, cos, sin, rotary):
+    """NeoX rotation of the first ``rotary`` elements, tail passed through (reference
+    model/layers.py:91-117, ``apply_rotary_emb_partial``)."""
+    return torch.cat([apply_rope(x[..., :rotary], cos, sin), x[..., rotary:]], dim=-1)
+
+
+@pytest.mark.parametrize("B,H,H_kv,D,rotary", [(32, 8, 2, 256, 64), (3, 8, 2, 256, 128), (4, 16, 8, 128, 64)])
+@pytest.mark.parametrize("zero_centred", [False, True], ids=["qwen3-norm", "qwen35-norm"])
+def test_partial_rope_and_the_zero_centred_norm(B, H, H_kv, D, rotary, zero_centred):
+    """Partial RoPE (Qwen3.5: 64 of 256 head dims rotate) and the zero-centred fp32 q/k
+    norm against their tensor-op restatements; the unrotated tail is the normed input."""
+    dtype, eps = torch.bfloat16, 1e-6
+    qkv, qn, kn, _, _, pos, slots = _case(B, H, H_kv, D, dtype, seed=B + rotary)
+    if zero_centred:  # a delta around zero, as the checkpoint's weights are
+        qn, kn = qn - 1.0, kn - 1.0
+    cos, sin = rope_table(rotary, 1e7, 4096, "cuda", dtype)
+    pool = PagedPool(1, 64, 16, H_kv, D, dtype=dtype, device="cuda", n_head=H, strict_writes=True)
+    q = pool.write_qk_norm_rope(0, slots, qkv, qn, kn, cos, sin, pos, eps, rotary_dim=rotary,
+                                zero_centred_norm=zero_centred)
+    torch.cuda.synchronize()
+    qr = qkv[:, : H * D].view(B, H, D)
+    kr = qkv[:, H * D:(H + H_kv) * D].view(B, H_kv, D)
+    vr = qkv[:, (H + H_kv) * D:].view(B, H_kv, D)
+    norm = (lambda x, w: _qwen35_norm(x, w, eps)) if zero_centred else (lambda x, w: rms_norm(x, w, eps))
+    c, s = cos[pos], sin[pos]  # (B, rotary/2); apply_rope inserts the head axis
+    q_want = _partial_rope(norm(qr, qn), c, s, rotary)
+    k_want = _partial_rope(norm(kr, kn), c, s, rotary)
+    flat_k = pool.keys[0].view(-1, H_kv, D)[slots]
+    assert torch.equal(pool.values[0].view(-1, H_kv, D)[slots], vr)
+    for got, want in ((q, q_want), (flat_k, k_want)):
+        same = (got == want).float().mean().item()
+        assert same > 0.995, f"only {same:.4%} of elements equal"
+        assert _ulps(got, want, dtype) <= 2.0
+        # the tail past rotary_dim is the normed input itself
+        assert _ulps(got[..., rotary:], want[..., rotary:], dtype) <= 1.0
+
+
+def test_partial_rope_rejects_unsupported_rotary_dims():
+    H, H_kv, D, dtype = 8, 2, 256, torch.bfloat16
+    qkv, qn, kn, _, _, pos, slots = _case(2, H, H_kv, D, dtype, seed=9)
+    cos, sin = rope_table(96, 1e7, 64, "cuda", dtype)
+    pool = PagedPool(1, 64, 16, H_kv, D, dtype=dtype, device="cuda", n_head=H)
+    with pytest.raises(ValueError, match="rotary_dim"):
+        pool.write_qk_norm_rope(0, slots, qkv, qn, kn, cos, sin, pos, 1e-6, rotary_dim=96)

@@ -151,7 +151,7 @@ def test_config3_packed_group_write_is_bit_exact(cuda):
     sinks_b = [PagedWriteSink(pool_b, t, n) for t, n in zip(inp.tables, inp.lengths)]
     positions = torch.cat([torch.arange(n) for n in inp.lengths]).to(cuda)
     packed = PackedPrefill(cu_seqlens=inp.cu_seqlens, positions=positions, sinks=sinks_a)
-    assert packed._packed_slots is not None
+    assert packed.group_slots is not None
     k = inp.k.to(cuda).unsqueeze(0)
     v = inp.v.to(cuda).unsqueeze(0)
     for layer in range(2):

@@ -1,15 +1,21 @@
 """Host-side contracts of the drop-in modules on a CPU-only host: validation messages,
-exception types and the no-fallback rule (reference tests/unit/test_triton_decode.py:
-405-460, tests/unit/test_attention_varlen.py:343-428, tests/unit/test_paged_kv.py:
-257-270,521-542, tests/unit/test_block_manager.py)."""
+exception types, the device-type dispatch and the no-fallback rule for HIP entry points
+(reference tests/unit/test_triton_decode.py:405-460, tests/unit/test_attention_varlen.py:
+343-449, tests/unit/test_paged_kv.py:134-183,257-287,521-542,
+tests/unit/test_packed_prefill.py:86-158). Host pools and the host prefill arm are
+built and used on ``cpu`` the way the reference's own CPU tests build them."""
 
 from __future__ import annotations
+
+import json
+from pathlib import Path
 
 import pytest
 import torch
 
 import miattn
-from miattn import BlockManager, HipVarlen, PackedPrefill, PagedKV, PagedPool, backend_for, paged_decode
+from miattn import (HipVarlen, PackedPrefill, PagedKV, PagedPool, PagedWriteSink, SdpaVarlen, backend_for,
+                    paged_decode)
 from miattn import decode as decode_mod
 
 
@@ -50,7 +56,7 @@ def test_paged_decode_raises_when_the_library_is_unavailable(monkeypatch):
 def test_decode_validation_errors_are_value_errors(mutate, match):
     args = mutate(_inputs())
     with pytest.raises(ValueError, match=match):
-        decode_mod._validate(*args)
+        decode_mod._check(*args)
 
 
 def test_varlen_validation_precedes_the_device_check():
@@ -82,13 +88,14 @@ def test_varlen_validation_precedes_the_device_check():
 
 
 def test_backend_selection_is_by_device_type():
-    with pytest.raises(ValueError, match="no packed-prefill backend"):
-        backend_for("cpu")
+    assert isinstance(backend_for("cpu"), SdpaVarlen) and backend_for("cpu").name == "sdpa-varlen"
+    assert isinstance(backend_for(torch.device("mps")), SdpaVarlen)
     with pytest.raises(ValueError, match="no packed-prefill backend"):
         backend_for("meta")
+    assert miattn.FlashVarlen is HipVarlen
 
 
-def test_pool_write_validation_and_no_cpu_write():
+def test_host_pool_write_validation():
     pool = PagedPool(2, 4, 16, 2, 4, n_head=4)
     k = torch.randn(2, 2, 4)
     slots = torch.tensor([0, 1])
@@ -102,14 +109,90 @@ def test_pool_write_validation_and_no_cpu_write():
         pool.write_slots(0, slots, k[:, :, :2], k[:, :, :2])
     with pytest.raises(IndexError, match="outside the pool's"):
         pool.write_slots(2, slots, k, k)
-    with pytest.raises(RuntimeError, match="no CPU fallback"):
-        pool.write_slots(0, slots, k, k)
+    with pytest.raises((IndexError, RuntimeError)):
+        pool.write_slots(0, torch.tensor([0, 10_000]), k, k)
     with pytest.raises(IndexError):
         pool.write_prefill(0, [0], 0, torch.randn(17, 2, 4), torch.randn(17, 2, 4))
     with pytest.raises(IndexError):
         pool.write_prefill(0, [pool.n_blocks], 0, k, k)
     with pytest.raises(ValueError):
         pool.write_prefill(0, [0], 0, k[:, :, :2], k)
+    pool.check_writes()  # host pools raise at the write; nothing pending
+
+
+def test_host_pool_writes_the_reference_known_answers():
+    """Slots of the reference's shuffled-table and block-boundary cases on a host pool
+    (tests/golden/slot_kats.json; reference tests/unit/test_paged_kv.py:134-158,464-478)."""
+    kats = json.loads((Path(__file__).parent / "golden" / "slot_kats.json").read_text())
+    case = kats["prefill_shuffled_table"]
+    bs, table = case["block_size"], case["block_table"]
+    pool = PagedPool(1, 8, bs, 2, 4)
+    k = torch.randn(case["length"], 2, 4)
+    v = torch.randn(case["length"], 2, 4)
+    pool.write_prefill(0, table, case["start"], k, v)
+    for t, block, offset in case["token_to_block_offset"]:
+        assert torch.equal(pool.keys[0][block, offset], k[t]) and torch.equal(pool.values[0][block, offset], v[t])
+    for block in case["untouched_blocks"]:
+        assert not pool.keys[0][block].any() and not pool.values[0][block].any()
+    edge = kats["decode_block_boundary"]
+    slots = PagedPool(1, 8, edge["block_size"], 2, 4).slot_ids(edge["block_table"], edge["position"], 1)
+    assert slots.tolist() == [edge["slot"]]
+    # int32 slot ids are accepted, as int64 are; the pool's flat view receives every row
+    pool.write_slots(0, torch.tensor([3, 17], dtype=torch.int32), k[:2], v[:2])
+    flat = pool.keys[0].view(-1, 2, 4)
+    assert torch.equal(flat[3], k[0]) and torch.equal(flat[17], k[1])
+
+
+def test_host_chunked_append_continues_a_request():
+    """A second chunk from start=21 lands after the first (reference
+    tests/unit/test_paged_kv.py:161-183)."""
+    pool = PagedPool(1, 6, 16, 2, 4)
+    table = [4, 1, 3]
+    first, second = torch.randn(21, 2, 4), torch.randn(19, 2, 4)
+    pool.write_prefill(0, table, 0, first, first)
+    pool.write_prefill(0, table, 21, second, second)
+    whole = torch.cat([first, second])
+    logical = pool.keys[0][torch.tensor(table)].reshape(-1, 2, 4)[:40]
+    assert torch.equal(logical, whole)
+
+
+def test_sdpa_arm_matches_the_longhand_oracle_and_isolates_segments():
+    from oracle.varlen import longhand_varlen
+
+    gen = torch.Generator().manual_seed(3)
+    cu = [0, 5, 6, 30]
+    q = torch.randn(30, 4, 16, generator=gen)
+    k = torch.randn(30, 2, 16, generator=gen)
+    v = torch.randn(30, 2, 16, generator=gen)
+    out = SdpaVarlen().prefill_varlen(q, k, v, cu_seqlens=cu, max_seqlen=24)
+    assert (out - longhand_varlen(q, k, v, cu)).abs().max().item() < 1e-5
+    k2 = k.clone()
+    k2[:5] += 1.0  # segment 0 only
+    out2 = SdpaVarlen().prefill_varlen(q, k2, v, cu_seqlens=torch.tensor(cu), max_seqlen=24)
+    assert torch.equal(out2[5:], out[5:])
+    with pytest.raises(ValueError, match="max_seqlen"):
+        SdpaVarlen().prefill_varlen(q, k, v, cu_seqlens=cu, max_seqlen=23)
+
+
+def test_packed_prefill_on_the_host_writes_through_paged_sinks():
+    """PackedPrefill on cpu picks the SDPA arm and writes each request through its sink
+    (reference tests/unit/test_packed_prefill.py:86-126)."""
+    pool = PagedPool(2, 8, 16, 2, 8, n_head=4)
+    lengths, tables = [5, 20], [[6], [2, 0]]
+    sinks = [PagedWriteSink(pool, t, n) for t, n in zip(tables, lengths)]
+    packed = PackedPrefill(cu_seqlens=[0, 5, 25], positions=torch.tensor(list(range(5)) + list(range(20))),
+                           sinks=sinks)
+    assert packed.backend_name == "sdpa-varlen" and packed.group_slots is not None
+    k = torch.randn(1, 25, 2, 8)
+    v = torch.randn(1, 25, 2, 8)
+    packed.write(1, k, v)
+    assert torch.equal(pool.keys[1][6, :5], k[0, :5])
+    assert torch.equal(pool.keys[1][2], k[0, 5:21]) and torch.equal(pool.values[1][0, :4], v[0, 21:])
+    with pytest.raises(RuntimeError, match="already written"):
+        packed.write(1, k, v)
+    q = torch.randn(1, 25, 4, 8)
+    y = packed.attend(q, k, v)
+    assert y.shape == (1, 25, 4, 8)
 
 
 def test_paged_kv_rejects_a_cpu_pool():
@@ -131,28 +214,6 @@ def test_packed_prefill_validation():
     p = PackedPrefill(cu_seqlens=[0, 2, 4], positions=torch.tensor([0, 1, 0, 1]), sinks=[object()] * 2,
                       backend=object())
     assert p.max_seqlen == 2 and p.last_token_index.tolist() == [1, 3] and p.n_seqs == 2
-
-
-def test_block_manager_contract():
-    m = BlockManager(4, 16)
-    assert m.reserve(2) == [0, 1]
-    assert m.reserve(3) is None and m.in_use == 2
-    assert m.reserve(0) == []
-    with pytest.raises(ValueError, match="duplicate"):
-        m.free([0, 0])
-    with pytest.raises(ValueError, match="not allocated"):
-        m.free([3])
-    assert m.in_use == 2, "a refused free changes nothing"
-    m.free([1])
-    assert m.reserve(2) == [1, 2]
-    assert m.peak == 3
-    assert m.blocks_for(0, 0) == 1 and m.blocks_for(16, 0) == 1 and m.blocks_for(16, 1) == 2
-    stats = m.stats()
-    assert stats["alloc_calls"] == 2 and stats["free_calls"] == 1 and stats["free"] == 1
-    with pytest.raises(ValueError):
-        BlockManager(0, 16)
-    with pytest.raises(ValueError):
-        m.reserve(-1)
 
 
 def test_availability_flag_is_exported():
