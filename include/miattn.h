@@ -32,7 +32,8 @@
  *   - the return value is MI_OK (0) or a negative MI_ERR_* code; mi_last_error() gives the
  *     message of the last failing call on the calling host thread;
  *   - no entry point allocates device memory: scratch space is a caller-owned workspace
- *     whose size the matching *_workspace_size() query returns;
+ *     whose size the matching *_workspace_size() query returns (mi_paged_decode_noalloc
+ *     uses a library-held device array instead);
  *   - launches are asynchronous on `stream`; nothing here synchronises the device.
  */
 #ifndef MIATTN_H_
@@ -216,6 +217,22 @@ int mi_paged_decode(const void* q, const void* k_cache, const void* v_cache,
                     int H, int H_kv, int D, int block_size, int max_blocks,
                     const int64_t* strides, float scale, int dtype, void* workspace,
                     size_t workspace_bytes, void* stream);
+
+/* mi_paged_decode_noalloc -- no counterpart in the reference: for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). mi_paged_decode with the same arguments minus the workspace: the
+ * split-K partials go to a device array the library holds per GPU, MI_DECODE_SCRATCH_BYTES
+ * (8 MiB; the Qwen3 shape fits up to B = 496 rows), from first use until the process ends.
+ * A shape whose mi_paged_decode_workspace_size() exceeds it returns MI_ERR_WORKSPACE.
+ * Nothing is allocated: the array's address on the current device is looked up once per
+ * device (hipGetSymbolAddress); `stream` must belong to the current device. Every call on
+ * one GPU shares that GPU's array, so calls that overlap on one GPU (several streams or host
+ * threads in flight at once) race: order them on one stream. */
+#define MI_DECODE_SCRATCH_BYTES (8u << 20)
+int mi_paged_decode_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                            const int32_t* block_table, const int32_t* seqlen, void* out, int B,
+                            int H, int H_kv, int D, int block_size, int max_blocks,
+                            const int64_t* strides, float scale, int dtype, void* stream);
 
 /* ------------------------------------------------------------------ varlen prefill
  * Replaces FlashVarlen.prefill_varlen (reference model/attention/varlen.py:317-357):

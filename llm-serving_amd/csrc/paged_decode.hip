@@ -35,6 +35,7 @@
 //   * K/V are read with the nontemporal hint: each byte is used once, and keeping it out
 //     of L2 lifted config 2 from 43.0 to 39.4 us and config 4 from 5.3 to 6.0 TB/s.
 // HBM-bound: per (token, KV head) the kernel reads 2 * D * esize bytes of K+V.
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -654,12 +655,15 @@ extern "C" size_t mi_paged_decode_workspace_size(int B, int H, int H_kv, int D, 
   return p.rows_bytes + p.ml_bytes + p.acc_bytes;
 }
 
-extern "C" int mi_paged_decode(const void* q, const void* k_cache, const void* v_cache,
-                               const int32_t* block_table, const int32_t* seqlen, void* out, int B,
-                               int H, int H_kv, int D, int block_size, int max_blocks,
-                               const int64_t* strides, float scale, int dtype, void* workspace,
-                               size_t workspace_bytes, void* stream) {
-  using namespace miattn;
+namespace miattn {
+namespace {
+
+// The body of both decode entry points; `workspace` is the caller's (mi_paged_decode) or
+// this GPU's scratch array (mi_paged_decode_noalloc).
+int paged_decode_entry(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
+                       const int32_t* seqlen, void* out, int B, int H, int H_kv, int D, int block_size,
+                       int max_blocks, const int64_t* strides, float scale, int dtype, void* workspace,
+                       size_t workspace_bytes, void* stream) {
   if (esize_of(dtype) == 0) return fail(MI_ERR_INVALID, "mi_paged_decode: unknown dtype %d", dtype);
   if (B < 0 || H < 1 || H_kv < 1 || H % H_kv != 0) {
     return fail(MI_ERR_INVALID, "mi_paged_decode: n_head (%d) must be a multiple of n_kv_head (%d)",
@@ -734,4 +738,79 @@ extern "C" int mi_paged_decode(const void* q, const void* k_cache, const void* v
     case MI_BF16: return dispatch_d<bf16_t>(D, q, k_cache, v_cache, block_table, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, s);
   }
   return fail(MI_ERR_INVALID, "mi_paged_decode: unknown dtype %d", dtype);
+}
+
+}  // namespace
+}  // namespace miattn
+
+// Split-K scratch of mi_paged_decode_noalloc: one array per GPU, held until the process
+// ends. Its name is a host-side stand-in; device code gets the address that
+// hipGetSymbolAddress returns for the current device (decode_scratch below).
+static __device__ __align__(256) unsigned char scratch[MI_DECODE_SCRATCH_BYTES];
+
+namespace miattn {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_addr[kMaxDevices] = {};
+
+// The current device's scratch address, looked up once per device with that device
+// current (no allocation: the array is part of the loaded code object).
+int decode_scratch(void** addr) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(MI_ERR_LAUNCH, "mi_paged_decode_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) {
+    return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode_noalloc: device %d is past the %d this library tracks", dev,
+                kMaxDevices);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_addr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      return fail(MI_ERR_LAUNCH, "mi_paged_decode_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                  hipGetErrorString(e));
+    }
+    g_scratch_addr[dev] = p;
+  }
+  *addr = g_scratch_addr[dev];
+  return MI_OK;
+}
+
+}  // namespace
+}  // namespace miattn
+
+extern "C" int mi_paged_decode(const void* q, const void* k_cache, const void* v_cache,
+                               const int32_t* block_table, const int32_t* seqlen, void* out, int B,
+                               int H, int H_kv, int D, int block_size, int max_blocks,
+                               const int64_t* strides, float scale, int dtype, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  return miattn::paged_decode_entry(q, k_cache, v_cache, block_table, seqlen, out, B, H, H_kv, D, block_size,
+                                    max_blocks, strides, scale, dtype, workspace, workspace_bytes, stream);
+}
+
+// The split-K partials need no clearing between calls: a row's (first slot, split count)
+// record is written by its first split before the merge launch reads it, every partial the
+// merge reads was written by this call's first launch, and rows of length 0 read nothing.
+extern "C" int mi_paged_decode_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                                       const int32_t* block_table, const int32_t* seqlen, void* out, int B,
+                                       int H, int H_kv, int D, int block_size, int max_blocks,
+                                       const int64_t* strides, float scale, int dtype, void* stream) {
+  using namespace miattn;
+  if (esize_of(dtype) != 0 && shape_ok(B, H, H_kv, D, block_size, max_blocks, dtype)) {
+    const size_t need = mi_paged_decode_workspace_size(B, H, H_kv, D, block_size, max_blocks, dtype);
+    if (need > MI_DECODE_SCRATCH_BYTES) {
+      return fail(MI_ERR_WORKSPACE,
+                  "mi_paged_decode_noalloc: this shape needs %zu bytes of split-K scratch, more than the %zu "
+                  "bytes the library holds per GPU; use mi_paged_decode with a workspace",
+                  need, size_t(MI_DECODE_SCRATCH_BYTES));
+    }
+  }
+  void* ws = nullptr;
+  const int rc = decode_scratch(&ws);
+  if (rc != MI_OK) return rc;
+  return paged_decode_entry(q, k_cache, v_cache, block_table, seqlen, out, B, H, H_kv, D, block_size, max_blocks,
+                            strides, scale, dtype, ws, MI_DECODE_SCRATCH_BYTES, stream);
 }

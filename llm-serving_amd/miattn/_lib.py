@@ -65,6 +65,11 @@ SIGNATURES: dict[str, tuple] = {
          _c_int, _c_int, _c_int, _c_int, _p_int64, _c_float, _c_int, _c_void_p, _c_size_t,
          _c_void_p],
     ),
+    "mi_paged_decode_noalloc": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int,
+         _c_int, _c_int, _c_int, _c_int, _p_int64, _c_float, _c_int, _c_void_p],
+    ),
     "mi_varlen_schedule": (
         _c_int, [_p_int32, _c_int, _c_int, _c_int, _c_int, _c_int, _p_int32, _c_int]
     ),
@@ -121,7 +126,7 @@ SIGNATURES: dict[str, tuple] = {
     ),
 }
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 
 def _load():
