@@ -313,6 +313,34 @@ def bench_tpot(stream, prompt_len: int = 1920, new_tokens: int = 128, B: int = 3
     }
 
 
+def bench_config5(stream, n_requests: int = 64, rate: float = 4.0, seed: int = 0) -> dict:
+    """Config 5 as specified: random-init Qwen3-0.6B served under a seeded Poisson trace (4
+    req/s, prompts lognormal(median 256, sigma 0.6) clipped to [32, 2048], uniform ids, 128
+    new tokens, greedy, max batch 32) by the continuous-batching loop (miattn.serve: FIFO
+    packed-group admission, one captured HIP graph over 32 seats, retirement at 128 tokens),
+    in real time. Reports TTFT and TPOT p50/p95 (nearest rank) over the requests."""
+    from miattn.qwen3 import Qwen3, Qwen3Config, random_weights
+    from miattn.serve import ContinuousServer, latency_summary, poisson_trace
+
+    cfg = Qwen3Config()
+    model = Qwen3(cfg, random_weights(cfg, seed), "cuda")
+    trace = poisson_trace(n_requests, rate=rate, vocab=cfg.vocab, max_new=128, seed=seed)
+    server = ContinuousServer(model, max_batch=32, n_blocks=8192, max_new=128, stream=None)
+    server.warm()
+    records, wall = server.run(trace, realtime=True)
+    out = latency_summary(records, wall)
+    out.update({
+        "workload": f"config5: {n_requests} requests, Poisson {rate} req/s (gamma shape 1, seed {seed}), prompts "
+                    "lognormal(median 256, sigma 0.6) clip [32,2048], 128 new tokens, greedy, max batch 32, "
+                    "block 16, continuous batching (one HIP graph over 32 seats), real time",
+        "decode_steps": server.steps_run,
+        "mean_prompt_tokens": sum(len(r.prompt) for r in trace) / max(1, len(trace)),
+    })
+    del server, model
+    torch.cuda.empty_cache()
+    return out
+
+
 def profiled_traffic() -> float | None:
     """HBM bytes per layer (split + merge launch) from the committed PMC summary
     (``profiles/paged_decode_config2_counters.json``): FETCH_SIZE and WRITE_SIZE per
@@ -466,7 +494,7 @@ def main() -> int:
         return 0
     stream = torch.cuda.Stream()
     if args.e2e_only:
-        print(json.dumps({"e2e": bench_tpot(stream)}), flush=True)
+        print(json.dumps({"e2e": bench_tpot(stream), "config5_trace": bench_config5(stream)}), flush=True)
         return 0
     if args.prefill_only:
         print(json.dumps({"prefill": bench_prefill(stream, args.steps, eager=args.eager)}), flush=True)
@@ -524,6 +552,10 @@ def main() -> int:
         line["tpot_ms"] = round(line["e2e"]["tpot_ms"], 4)
         log(f"TPOT {line['tpot_ms']:.3f} ms (eager step {line['e2e']['eager_step_ms']:.2f} ms)")
         torch.cuda.empty_cache()
+        log("config 5: continuous batching under a Poisson trace (real time)")
+        line["config5_trace"] = bench_config5(stream)
+        log(f"config5: TTFT p50 {line['config5_trace']['ttft_p50_ms']:.1f} ms, "
+            f"TPOT p50 {line['config5_trace']['tpot_p50_ms']:.3f} ms")
         log("long-context decode (config 4)")
         line["long_context"] = bench_long_context(stream)
         log(f"config4: {line['long_context']['gbs']:.1f} GB/s")

@@ -98,7 +98,8 @@ int mi_kv_slot_write(const void* k, const void* v, const void* slot_ids, int slo
  * (64, 128 or 256, <= D; the rest pass through, model/layers.py:91-117) with the
  * (n_pos, rotary_dim/2) cos/sin tables at row pos[b] (int64), each product and sum rounded
  * to the activation dtype (see csrc/decode_epilogue.hip). slot_ids as for mi_kv_slot_write (int32 or
- * int64 per slot_bits; pools (n_slots, H_kv, D) contiguous). A row whose position is outside
+ * int64 per slot_bits; pools (n_slots, H_kv, D) contiguous). A row with slot -1 has nothing to
+ * write this step and is skipped silently; any other row whose position is outside
  * [0, n_pos) or whose slot is outside [0, n_slots) is not written and 1 + its index goes to
  * *error_word (may be NULL). D = 64, 128 or 256. qkv_parts = 0: qkv holds `dtype` values;
  * qkv_parts = n >= 1: qkv holds fp32 split-K partial sums [n][B][row_stride] (mi_rows_gemm
@@ -140,7 +141,8 @@ int mi_argmax_rows(const void* x, int64_t ld, int rows, int cols, int64_t* out, 
  * (reference: the slot map model/paged.py:474-501, the embedding lookup and layer 0's input
  * norm model/minillm.py:111-136, model/layers.py:342-350, the generate loop's argmax and
  * position advance).
- * mi_decode_step_begin, per row b (block_table (B, >= max_blocks) int32, row stride bt_stride):
+ * mi_decode_step_begin, per row b (block_table (B, >= max_blocks) int32, row stride bt_stride;
+ * a row with pos[b] < 0 is an idle seat: made inert as below without a report):
  *   seqlen[b] = pos[b] + 1;  slots[b] = table[b, pos[b] / block_size] * block_size + pos[b] % block_size;
  *   x[b] = embed[tokens[b]] (embed (vocab, cols));  h[b] = x[b] / sqrt(mean(x[b]^2) + eps) * norm_w,
  *   rounded as mi_add_rms_norm. A row whose token is outside [0, vocab), whose position is
@@ -150,7 +152,7 @@ int mi_argmax_rows(const void* x, int64_t ld, int rows, int cols, int64_t* out, 
  *   x = h = 0), so no later launch of the step writes or reads pool memory for it.
  * mi_greedy_advance: pick[r] = argmax of logits row r as mi_argmax_rows; tokens[r] = pick;
  *   history[r * hist_stride + steps[r]] = pick while 0 <= steps[r] < max_steps; steps[r] += 1;
- *   pos[r] += 1 (all int64). */
+ *   pos[r] += 1 (all int64); a row with pos[r] < 0 (an idle seat) is left unchanged. */
 int mi_decode_step_begin(const int64_t* tokens, const int64_t* pos, const int32_t* block_table, int64_t bt_stride,
                          int block_size, int max_blocks, const void* embed, int64_t vocab, const void* norm_w,
                          int cols, float eps, int32_t* seqlen, int64_t* slots, void* x, void* h, int B, int dtype,

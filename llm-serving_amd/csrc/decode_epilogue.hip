@@ -66,10 +66,13 @@ __global__ __launch_bounds__(256) void qk_norm_rope_write_kernel(
   const int b = blockIdx.x;
   const int n_heads = H + 2 * H_kv;
   if (head >= n_heads || b >= B) return;  // wave-uniform
-  // a row whose position is outside the RoPE table or whose slot is outside the pool is
-  // not written at all and is reported (row + 1) through the error word
+  // slot -1 marks a row with nothing to write this step (an idle or refused seat of a decode
+  // step): skipped silently. Any other row whose position is outside the RoPE table or whose
+  // slot is outside the pool is not written at all and is reported (row + 1) through the
+  // error word.
   const int64_t pb = pos[b];
   const IdxT slot = slots[b];
+  if (slot == IdxT(-1)) return;
   if (pb < 0 || pb >= n_pos || !(slot >= 0 && int64_t(slot) < n_slots)) {
     if (lane == 0 && head == 0 && err != nullptr) atomicCAS(err, 0, b + 1);
     return;

@@ -126,13 +126,14 @@ __global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(
 // Start of a captured decode step, one workgroup per row: seqlen = pos + 1, the row's write
 // slot table[pos / bs] * bs + pos % bs (reference model/paged.py:499-501), x = embed[token]
 // (the embedding lookup) and h = rmsnorm(x) * w (layer 0's input norm).
-// A row is refused when its token is outside the vocabulary, its position is negative or
-// past the table's width, or the table entry for its position is negative (a row's table
-// padded with -1 past its own blocks, so a row that runs past its own blocks is caught
-// even inside a wider batch table). A refused row is reported (row + 1) through the error
-// word and made inert for the rest of the step: slot -1 (every later write of the row is
-// skipped and reported by its own launch), seqlen 0 (its attention reads nothing and is
-// zero) and x = h = 0; no other row's state is touched.
+// A row with a negative position is an idle seat of a serving batch: it is made inert for
+// the step (below) without a report. A row is refused when its token is outside the
+// vocabulary, its position is past the table's width, or the table entry for its position
+// is negative (a row's table padded with -1 past its own blocks, so a row that runs past
+// its own blocks is caught even inside a wider batch table); it is reported (row + 1)
+// through the error word and made inert. Inert: slot -1 (the epilogue writes nothing for
+// the row), seqlen 0 (its attention reads nothing and is zero) and x = h = 0; no other
+// row's state is touched.
 template <typename T, int PER>
 __global__ __launch_bounds__(kNormThreads) void step_begin_kernel(
     const int64_t* __restrict__ tokens, const int64_t* __restrict__ pos, const int32_t* __restrict__ table,
@@ -143,11 +144,12 @@ __global__ __launch_bounds__(kNormThreads) void step_begin_kernel(
   const int tid = threadIdx.x;
   const int64_t t = tokens[row];
   const int64_t p = pos[row];
-  const bool in_table = p >= 0 && p / block_size < max_blocks;
+  const bool idle = p < 0;
+  const bool in_table = !idle && p / block_size < max_blocks;
   const int32_t page = in_table ? table[row * bt_stride + p / block_size] : -1;
-  if (t < 0 || t >= vocab || page < 0) {  // uniform over the workgroup
+  if (idle || t < 0 || t >= vocab || page < 0) {  // uniform over the workgroup
     if (tid == 0) {
-      if (err != nullptr) atomicCAS(err, 0, row + 1);
+      if (!idle && err != nullptr) atomicCAS(err, 0, row + 1);
       seqlen[row] = 0;
       slots[row] = -1;
     }
@@ -284,7 +286,7 @@ __device__ __forceinline__ void finish_pick(Best b, Best* part, int row, int64_t
       if (better(part[k].v, part[k].i, r)) r = part[k];
     }
     if (out != nullptr) out[row] = r.i;
-    if (adv.tokens != nullptr) {
+    if (adv.tokens != nullptr && adv.pos[row] >= 0) {  // an idle seat (pos < 0) keeps its state
       adv.tokens[row] = r.i;
       const int64_t st = adv.steps[row];
       if (st >= 0 && st < adv.max_steps) adv.history[row * adv.hist_stride + st] = r.i;

@@ -1,24 +1,28 @@
 """End to end: random-init Qwen3-0.6B on the HIP attention path vs the CPU seat path.
 
-The CPU seat path's greedy run (``tests/golden/qwen3_greedy_seed0.json``, made by
-``tests/golden/make_qwen3_greedy.py`` with ``oracle.qwen3_seat``) is the reference. The
-GPU model runs the same weights with packed prefill (HIP varlen kernel + packed slot
-write) and paged decode (HIP slot write + block-table decode) through the reference's
-containers.
+The gate is the reference's (``results/W45/0001-paged-packed-numeric-gate/config.toml:9``):
+greedy tokens must equal the CPU seat path's, and a miss counts only if it is not a near-tie
+under an fp32 recomputation of that step. ``tests/golden/greedy_gate_seed0.json`` (made by
+``tests/golden/make_greedy_gate.py``) holds the bf16 seat path's tokens and, for every step,
+the fp32 logits of the candidate tokens on the same context plus ``bf16_err``, how far the
+bf16 computation strays from fp32 there. A GPU token ``g`` that differs from the CPU token
+``c`` is a near-tie when ``fp32[g] >= fp32[c] - 2 * bf16_err``: two bf16 computations that
+each stray by up to ``bf16_err`` can order such a pair either way (the CPU bf16 path itself
+disagrees with fp32 on 8 of the closed case's 260 steps). Every miss must be one; the
+exact-agreement count is asserted as a floor and reported.
 
-Random N(0, 0.02) weights make the logits flat: the reference's own logits are bf16 and
-tie exactly at the top in 9 of the fixture's 260 steps and come within 0.05 in 78. Two
-implementations that round their bf16 GEMMs differently (CPU vs GPU BLAS) therefore cannot
-agree on every argmax by construction. The gate is teacher-forced: at every one of the 65
-steps (prefill + 64 decode) of every row, fed the CPU path's token, the GPU argmax must be
-a token whose CPU logit is within TIE_TOL of the CPU maximum (exact agreement is counted
-and reported). Free-running greedy must agree exactly up to the first step where the CPU
-run itself had a near-tie.
+* closed case (4 prompts, 64 decode steps): teacher-forced on the CPU tokens, every step's
+  GPU argmax is compared; free-running greedy on the captured graph must agree exactly up
+  to the row's first teacher-forced miss (the contexts are identical until then);
+* trace case (config 5 sized down: 8 Poisson requests, 32 tokens each): served by the
+  continuous-batching loop (``miattn.serve``), each request's tokens must agree up to its
+  first divergence, which must be a near-tie.
 """
 
 from __future__ import annotations
 
 import json
+import warnings
 from pathlib import Path
 
 import pytest
@@ -26,13 +30,15 @@ import torch
 
 from miattn import PagedKV
 from miattn.qwen3 import GraphDecoder, Qwen3, Qwen3Config, random_weights
+from miattn.serve import ContinuousServer, TraceRequest
 
 pytestmark = pytest.mark.gpu
 
-FIX = json.loads((Path(__file__).parent / "golden" / "qwen3_greedy_seed0.json").read_text())
-STEPS = len(FIX["steps"]) - 1
-TIE_TOL = 0.0625  # 4 bf16 ulps of a logit in [2, 4): the CPU path's own rounding scale
+FIX = json.loads((Path(__file__).parent / "golden" / "greedy_gate_seed0.json").read_text())
+CLOSED, TRACE = FIX["closed"], FIX["trace"]
+STEPS = CLOSED["steps"]
 BS = 16
+MIN_EXACT = 0.95  # floor on exact agreement; every miss must also be an fp32 near-tie
 
 
 @pytest.fixture(scope="module")
@@ -52,47 +58,38 @@ def _tables(lengths, extra, seed=11):
     return tables, 4 * sum(need)
 
 
-def _allowed(step, row):
-    ids, logits = step["ids"][row], step["logits"][row]
-    return {i for i, v in zip(ids, logits) if v >= logits[0] - TIE_TOL}
+def near_tie(case, step: int, row: int, gpu_token: int) -> bool:
+    """Whether a GPU token that differs from the CPU one is a genuine near-tie in fp32."""
+    ids, vals = case["cand_ids"][step][row], case["cand_fp32"][step][row]
+    fp32 = dict(zip(ids, vals))
+    cpu_token = case["tokens"][row][step]
+    if gpu_token not in fp32:
+        return False
+    return fp32[gpu_token] >= fp32[cpu_token] - 2.0 * case["bf16_err"][step][row]
 
 
-def _prefill(model, tables, n_blocks):
+def _prefill(model, case, tables, n_blocks):
     pool = model.new_pool(n_blocks, BS)
-    logits = model.prefill(FIX["prompts"], pool, tables)
-    return pool, logits
+    return pool, model.prefill(case["prompts"], pool, tables)
 
 
-def test_teacher_forced_greedy_agrees_with_cpu_seat_path(model):
-    lengths = FIX["lengths"]
+def _teacher_forced_argmax(model):
+    """The GPU's greedy pick at every step of the closed case, fed the CPU tokens."""
+    lengths = CLOSED["lengths"]
     tables, n_blocks = _tables(lengths, STEPS + 1)
-    pool, logits = _prefill(model, tables, n_blocks)
+    pool, logits = _prefill(model, CLOSED, tables, n_blocks)
     paged = PagedKV(pool, tables, lengths, rope_len=max(lengths) + STEPS + 1, n_head=model.cfg.n_head)
-    exact = ok = 0
-    worst = 0.0
-    for s in range(STEPS + 1):
-        if s:
-            forced = torch.tensor([FIX["tokens"][r][s - 1] for r in range(len(lengths))], device="cuda")
-            logits = model.decode(paged, forced)
-        got = logits.float().argmax(-1).tolist()
-        step = FIX["steps"][s]
-        for r, g in enumerate(got):
-            ids = torch.tensor(step["ids"][r], device="cuda")
-            worst = max(worst, (logits[r, ids].float().cpu() - torch.tensor(step["logits"][r])).abs().max().item())
-            assert g in _allowed(step, r), (
-                f"step {s} row {r}: GPU argmax {g} is not within {TIE_TOL} of the CPU maximum "
-                f"(CPU top ids {step['ids'][r][:4]}, logits {step['logits'][r][:4]})")
-            ok += 1
-            exact += g == step["argmax"][r]
-    print(f"teacher-forced: {ok}/{ok} steps within tie tolerance, {exact}/{ok} exact argmax, "
-          f"max |GPU - CPU| over the CPU top-16 logits {worst:.4f}")
-    assert worst <= 4 * TIE_TOL
+    picks = [logits.float().argmax(-1).tolist()]
+    for s in range(STEPS):
+        forced = torch.tensor([CLOSED["tokens"][r][s] for r in range(len(lengths))], device="cuda")
+        picks.append(model.decode(paged, forced).float().argmax(-1).tolist())
+    return [[picks[s][r] for s in range(STEPS + 1)] for r in range(len(lengths))]
 
 
 def _free_run(model, use_graph):
-    lengths = FIX["lengths"]
+    lengths = CLOSED["lengths"]
     tables, n_blocks = _tables(lengths, STEPS + 1)
-    pool, logits = _prefill(model, tables, n_blocks)
+    pool, logits = _prefill(model, CLOSED, tables, n_blocks)
     first = logits.argmax(-1)
     if use_graph:
         dec = GraphDecoder(model, pool, tables, lengths, first, STEPS)
@@ -112,20 +109,64 @@ def _free_run(model, use_graph):
     return torch.cat([first.cpu().view(-1, 1), rest], 1)
 
 
-def test_free_running_greedy_matches_until_the_first_near_tie(model):
-    got = _free_run(model, use_graph=False)
-    for r in range(len(FIX["lengths"])):
-        first_tie = next((s for s, st in enumerate(FIX["steps"])
-                          if st["logits"][r][0] - st["logits"][r][1] < TIE_TOL), STEPS + 1)
-        agree = next((s for s in range(STEPS + 1) if got[r, s].item() != FIX["tokens"][r][s]), STEPS + 1)
-        print(f"row {r}: free-running agreement {agree}/{STEPS + 1} steps (first CPU near-tie at {first_tie})")
-        assert agree >= first_tie
+def test_greedy_gate_closed_case(model):
+    """Teacher-forced: every step's pick equals the CPU seat path's or is an fp32 near-tie;
+    free-running on the captured graph: equal up to each row's first teacher-forced miss."""
+    forced = _teacher_forced_argmax(model)
+    total = exact = 0
+    misses = []
+    for r, row in enumerate(forced):
+        for s, g in enumerate(row):
+            total += 1
+            if g == CLOSED["tokens"][r][s]:
+                exact += 1
+            else:
+                misses.append((r, s, g))
+    unresolved = [m for m in misses if not near_tie(CLOSED, m[1], m[0], m[2])]
+    free = _free_run(model, use_graph=True)
+    prefix = []
+    for r, row in enumerate(forced):
+        first_miss = next((s for s, g in enumerate(row) if g != CLOSED["tokens"][r][s]), STEPS + 1)
+        agree = next((s for s in range(STEPS + 1) if free[r, s].item() != CLOSED["tokens"][r][s]), STEPS + 1)
+        prefix.append(f"{agree}/{STEPS + 1}")
+        assert agree == first_miss, f"row {r}: free-running diverged at {agree}, teacher-forced first miss {first_miss}"
+    warnings.warn(f"greedy gate (closed): {exact}/{total} steps exact, {len(misses) - len(unresolved)} fp32 "
+                  f"near-ties, {len(unresolved)} unresolved; free-running exact prefix per row {prefix}")
+    assert not unresolved, f"misses that are not fp32 near-ties (row, step, gpu token): {unresolved}"
+    assert exact >= MIN_EXACT * total, f"only {exact}/{total} exact"
 
 
 def test_graph_replayed_decode_equals_eager_decode(model):
     eager = _free_run(model, use_graph=False)
     graph = _free_run(model, use_graph=True)
     assert torch.equal(eager, graph)
+
+
+def test_greedy_gate_continuous_batching_trace(model):
+    """Config 5 sized down: the fixture's 8 Poisson requests served by the continuous-batching
+    loop (packed group prefill on admission, one captured graph over 32 seats, retirement at
+    32 tokens); each request's tokens equal the CPU seat path's up to a first divergence
+    that is an fp32 near-tie."""
+    trace = [TraceRequest(i, a, tuple(p), TRACE["max_new"])
+             for i, (a, p) in enumerate(zip(TRACE["arrivals"], TRACE["prompts"]))]
+    server = ContinuousServer(model, max_batch=32, n_blocks=2048, max_new=TRACE["max_new"])
+    server.warm()
+    records, _ = server.run(trace, realtime=False)
+    exact = total = 0
+    report = []
+    for rec in records:
+        want = TRACE["tokens"][rec.idx]
+        assert len(rec.tokens) == len(want) == TRACE["max_new"]
+        div = next((s for s, (g, c) in enumerate(zip(rec.tokens, want)) if g != c), len(want))
+        exact += div
+        total += len(want)
+        report.append(f"{div}/{len(want)}")
+        if div < len(want):
+            assert near_tie(TRACE, div, rec.idx, rec.tokens[div]), (
+                f"request {rec.idx}: token {div} is {rec.tokens[div]}, CPU {want[div]}, not an fp32 near-tie")
+        assert rec.ttft_ms == rec.ttft_ms and rec.tpot_ms > 0
+    warnings.warn(f"greedy gate (trace): exact prefixes {report}; {exact}/{total} tokens before any divergence")
+    assert server.steps_run >= TRACE["max_new"] - 1
 
 
 def test_graph_step_past_one_rows_blocks_touches_no_other_row(model):
