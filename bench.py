@@ -372,6 +372,21 @@ def copy_calibration(mib: int, reps: int) -> dict:
             "gbs_read_plus_write": 2 * n * 2 / dt / 1e9}
 
 
+def bench_block32(stream, steps: int = 50) -> dict:
+    """Config 2 with 32-token blocks (the reference's other contract block size): the same
+    lengths and the same bytes in 4096 blocks of 32 per layer, checked then timed like the
+    headline leg."""
+    from miattn import workloads as W
+
+    inp = W.paged_decode_config(device="cuda", block_size=32, n_blocks=4096)
+    res = bench_decode(inp, steps, 5, stream)
+    res.pop("out0")
+    del inp
+    torch.cuda.empty_cache()
+    return {"workload": "config2 lengths, block size 32 (4096 blocks/layer), 28 layers, HIP-graph replay", **res,
+            "frac_hbm_peak": res["gbs"] / HBM_PEAK_GBS}
+
+
 def check_decode_rows(inp, out0, rows) -> float:
     """Layer 0's output rows ``rows`` against the fp32 gather oracle (oracle.decode), before
     anything is timed; returns max|delta| and exits when it is outside the bf16 bar."""
@@ -439,6 +454,8 @@ def cpu_baseline(inp, gpu_out0, budget_s: float = 10.0):
         times.append(time.perf_counter() - t0)
     p50 = percentile(times, 0.5)
     nbytes = decode_bytes(inp.lengths, B, H, H_kv, D, inp.block_table.shape[1])
+    c1 = cpu_config1(budget_s / 2)
+    c5 = cpu_config5_step()
     cpu_model = "unknown"
     try:
         for line in open("/proc/cpuinfo"):
@@ -457,7 +474,63 @@ def cpu_baseline(inp, gpu_out0, budget_s: float = 10.0):
         "ms_per_layer_p50": p50 * 1e3,
         "cpu_model": cpu_model,
         "gpu_vs_seat_max_abs_diff": max_diff,
+        "config1": c1,
+        "config5_decode_step": c5,
     }
+
+
+def cpu_config1(budget_s: float) -> dict:
+    """Config 1 on the CPU seat path: one layer of B=8 rows, 511 cached + 1 new token, RoPE
+    pre-applied (miattn.workloads.seat_decode_config1), timed on all host threads;
+    algorithmic bytes B * 512 * 2 * H_kv * D * 2 = 16.8 MB."""
+    from miattn import workloads as W
+    from oracle.seat import SeatSlab
+
+    q, k, v = W.seat_decode_config1()
+    B, H_kv, L, D = k.shape
+    slab = SeatSlab(1, B, H_kv, D, L, dtype=k.dtype, n_head=q.shape[1])
+    slab.keys[0].copy_(k)
+    slab.values[0].copy_(v)
+    for b in range(B):
+        slab.activate(b, L)
+    slab.build_mask(next_token=False)
+    times = []
+    deadline = time.perf_counter() + budget_s
+    while time.perf_counter() < deadline or len(times) < 20:
+        t0 = time.perf_counter()
+        slab.attend(0, q)
+        times.append(time.perf_counter() - t0)
+    p50 = percentile(times, 0.5)
+    nbytes = B * L * 2 * H_kv * D * k.element_size()
+    return {"us_per_step_p50": p50 * 1e6, "us_per_step_p95": percentile(times, 0.95) * 1e6,
+            "gbs": nbytes / p50 / 1e9, "bytes": nbytes, "samples": len(times),
+            "sample": "config1: one seat-path decode layer, B=8 x 512 tokens, H16/8 D128 bf16"}
+
+
+def cpu_config5_step(B: int = 32, prompt: int = 128, steps: int = 3) -> dict:
+    """A few B=32 greedy decode steps of the random-init Qwen3-0.6B on the CPU seat path
+    (oracle.qwen3_seat: slab KV, SDPA prefill, bf16 softmax decode), prompts of ``prompt``
+    uniform tokens; ms per whole decode step (28 layers + lm_head)."""
+    from miattn.qwen3 import Qwen3Config, random_weights
+    from oracle.qwen3_seat import SeatQwen3
+
+    cfg = Qwen3Config()
+    model = SeatQwen3(cfg, random_weights(cfg, 0), B, prompt + steps + 2)
+    gen = torch.Generator().manual_seed(1)
+    t0 = time.perf_counter()
+    first = torch.stack([model.prefill(r, torch.randint(0, cfg.vocab, (prompt,), generator=gen).tolist())
+                         for r in range(B)])
+    prefill_s = time.perf_counter() - t0
+    tok = first.argmax(-1)
+    times = []
+    for _ in range(steps + 1):
+        t0 = time.perf_counter()
+        tok = model.decode(tok).argmax(-1)
+        times.append(time.perf_counter() - t0)
+    times = times[1:]  # the first step warms the host allocator
+    return {"ms_per_step_p50": percentile(times, 0.5) * 1e3, "steps": len(times), "prefill_s": prefill_s,
+            "sample": f"config5 shape on the CPU: B={B} rows, {prompt}-token prompts (context {prompt}->"
+                      f"{prompt + steps + 1}), bf16 seat path, {steps} timed steps after one warm step"}
 
 
 def main() -> int:
@@ -556,6 +629,9 @@ def main() -> int:
         line["config5_trace"] = bench_config5(stream)
         log(f"config5: TTFT p50 {line['config5_trace']['ttft_p50_ms']:.1f} ms, "
             f"TPOT p50 {line['config5_trace']['tpot_p50_ms']:.3f} ms")
+        log("block size 32 (config 2 lengths)")
+        line["decode_block32"] = bench_block32(stream)
+        log(f"bs32: {line['decode_block32']['us_per_layer']:.2f} us/layer")
         log("long-context decode (config 4)")
         line["long_context"] = bench_long_context(stream)
         log(f"config4: {line['long_context']['gbs']:.1f} GB/s")

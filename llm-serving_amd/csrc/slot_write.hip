@@ -9,8 +9,8 @@
 // contiguous whenever the source row is. Algorithmic traffic is 2 * n_tokens * H_kv * D *
 // esize read + the same written. Loads and stores carry the nontemporal hint: each byte is
 // touched once here; the written slots are next read a decode step later, and the prefill
-// that follows reads the source rows, but a packed group's K/V (30 MB at 3711 tokens) is
-// far more than one XCD's 4 MB L2 (measured on that group: 10.06 -> 9.30 us, the prefill
+// that follows reads the source rows, but a packed group's K/V (17.7 MB at 4311 tokens, 35 MB
+// read and written) is far more than one XCD's 4 MB L2 (measured on that group: 10.06 -> 9.30 us, the prefill
 // after it unchanged; more chunks per thread, 2/4/8 with all loads first, measured slower:
 // 10.2/10.6/11.7 us).
 // Sources with a non-unit element stride or 16-byte misalignment take the scalar kernel

@@ -57,6 +57,8 @@ SHAPES = [
     pytest.param(4, 16, 8, 128, 16, [2048, 700, 129, 5], id="qwen3-b4"),
     pytest.param(2, 16, 8, 128, 16, [8192, 3001], id="qwen3-long-splitk"),
     pytest.param(2, 8, 4, 32, 16, [77, 300], id="d32"),
+    pytest.param(6, 8, 2, 256, 16, [2048, 1, 700, 129, 0, 3000], id="qwen35-h8-kv2-d256"),
+    pytest.param(3, 8, 2, 256, 32, [1664, 33, 4097], id="qwen35-h8-kv2-d256-bs32"),
     pytest.param(2, 4, 2, 16, 16, [50, 33], id="d16"),
 ]
 
