@@ -37,6 +37,7 @@ HBM_PEAK_GBS = 8000.0
 BF16_MFMA_PEAK_TFLOPS = 2500.0
 METRIC = "paged-decode attn HBM GB/s (% peak) + TPOT ms, Qwen3-0.6B B=32 ctx2048"
 N_LAYER = 28
+WARM_MS = 300.0  # untimed replays before each timed graph block
 
 
 def log(msg: str) -> None:
@@ -84,6 +85,12 @@ def time_graph(step, stream, steps: int, warmup: int):
     samples = []
     with torch.cuda.stream(stream):
         for _ in range(warmup):
+            graph.replay()
+        # then at least WARM_MS of untimed replays: a short graph (one prefill step is under
+        # a millisecond) would otherwise be timed while the clocks are still ramping
+        with EventTimer(stream) as one:
+            graph.replay()
+        for _ in range(int(WARM_MS / max(one.ms(), 1e-3))):
             graph.replay()
         torch.cuda.synchronize()
         with EventTimer(stream) as total:

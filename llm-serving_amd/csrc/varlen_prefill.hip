@@ -1221,6 +1221,17 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
         lsum += p;
       }
       l_i = fmaf(l_i, alpha, lsum);
+      // P(t) packed here, in the block of this step's MFMAs, and pinned: left alone the
+      // compiler sinks the exponentials past the end of the step, beside the PV MFMAs that
+      // read P, where nothing hides them (2-3% of the kernel)
+      uint4 pN[2];
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2) {
+        pN[t2] = make_uint4(pack2<T>(sc[8 * t2 + 0], sc[8 * t2 + 1]), pack2<T>(sc[8 * t2 + 2], sc[8 * t2 + 3]),
+                            pack2<T>(sc[8 * t2 + 4], sc[8 * t2 + 5]), pack2<T>(sc[8 * t2 + 6], sc[8 * t2 + 7]));
+      }
+      asm volatile("" : "+v"(pN[0].x), "+v"(pN[0].y), "+v"(pN[0].z), "+v"(pN[0].w),
+                        "+v"(pN[1].x), "+v"(pN[1].y), "+v"(pN[1].z), "+v"(pN[1].w));
       floatx16 nxt = zero16();
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) nxt = mfma32<T>(kf[ks], qB[ks], nxt);
@@ -1246,11 +1257,8 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
 #pragma unroll
         for (int i = 0; i < DB; ++i) o[i] *= alpha;
       }
-#pragma unroll
-      for (int t2 = 0; t2 < 2; ++t2) {
-        pB[t2] = make_uint4(pack2<T>(sc[8 * t2 + 0], sc[8 * t2 + 1]), pack2<T>(sc[8 * t2 + 2], sc[8 * t2 + 3]),
-                            pack2<T>(sc[8 * t2 + 4], sc[8 * t2 + 5]), pack2<T>(sc[8 * t2 + 6], sc[8 * t2 + 7]));
-      }
+      pB[0] = pN[0];
+      pB[1] = pN[1];
       cur = nxt;
       __builtin_amdgcn_s_setprio(0);
       wait_vm_lgkm0<0>();
