@@ -966,6 +966,9 @@ template <int D>
 struct Duo {
   static constexpr int WAVES = 4;             // 2 query blocks x 2 key halves
   static constexpr int THREADS = 64 * WAVES;
+  // workgroups per CU: two at head_dim 64/128; one at 256 (128 KiB of K/V buffers, and the
+  // 32 x 256 O^T accumulator and Q operands need the 512 registers of a lone wave per SIMD)
+  static constexpr int PER_CU = D == 256 ? 1 : 2;
   static constexpr int BQ = 64;               // query rows per item
   static constexpr int BK = 64;               // keys per step
   static constexpr int ROWB = D * 2;          // bytes of one key row of one KV head
@@ -974,13 +977,20 @@ struct Duo {
   static constexpr int SEGS = BUFB / 1024;    // 1 KiB wave-wide loads per buffer
   static constexpr int LPW = SEGS / WAVES;    // of them per wave
   static constexpr int RPS = 1024 / ROWB;     // key rows per wave-wide load
-  static constexpr int SWB = NCH == 16 ? 4 : 3;
+  static constexpr int SWB = NCH >= 16 ? 4 : 3;
+  // rows after which the swizzle repeats (it permutes the low SWB bits of the chunk index:
+  // the 64 banks cover 256 bytes, so a 512-byte row's two halves alias)
+  static constexpr int SW_PERIOD = 1 << SWB;
+  // wave-wide loads i and i + LOAD_PERIOD of a wave land rows a whole swizzle period apart,
+  // so their lane offsets differ by a constant
+  static constexpr int LOAD_PERIOD = (WAVES * RPS) % SW_PERIOD == 0 ? 1 : SW_PERIOD / (WAVES * RPS);
   static constexpr int ITEM_WORDS = 4;        // {seq0, L, tile << 16 | split << 8 | n_split - 1, h << 24 | slot}
-  static_assert(D == 64 || D == 128, "duo kernel head dims");
-  static_assert(SEGS % WAVES == 0 && (WAVES * RPS) % NCH == 0, "whole loads per wave, swizzle invariant");
+  static_assert(D == 64 || D == 128 || D == 256, "duo kernel head dims");
+  static_assert(SEGS % WAVES == 0 && LPW % LOAD_PERIOD == 0 && (WAVES * RPS * LOAD_PERIOD) % SW_PERIOD == 0,
+                "whole loads per wave, swizzle periodic in the loads");
   static_assert(2 * (D / 32) * 16 * 64 * 4 <= 2 * BUFB, "fold fits the V ring");
   static constexpr __host__ __device__ int sw(int r) {
-    return ((r & 3) << (SWB - 2)) | ((r >> 2) & ((NCH >> 2) - 1));
+    return ((r & 3) << (SWB - 2)) | ((r >> 2) & ((1 << (SWB - 2)) - 1));
   }
 };
 
@@ -988,7 +998,7 @@ struct Duo {
 __device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14)); }
 
 template <typename T, int D>
-__global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
+__global__ __launch_bounds__(Duo<D>::THREADS, Duo<D>::PER_CU) void varlen_prefill_duo_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     T* __restrict__ out, const int32_t* __restrict__ sched, float* __restrict__ partials, int H, int H_kv,
     int G, float scale_log2, int causal) {
@@ -996,10 +1006,11 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
   constexpr int KS = D / 16;  // MFMA k-steps over D for S^T
   constexpr int DB = D / 32;  // 32-row blocks of D for O^T
   constexpr int BK = W::BK, BQ = W::BQ, ROWB = W::ROWB, LPW = W::LPW;
-  __shared__ __align__(16) uint8_t kb0[W::BUFB];
-  __shared__ __align__(16) uint8_t kb1[W::BUFB];
-  __shared__ __align__(16) uint8_t vb0[W::BUFB];
-  __shared__ __align__(16) uint8_t vb1[W::BUFB];
+  // 512-byte aligned: at head_dim 256 the operand offsets are XOR-swizzled in bits 4-8
+  __shared__ __align__(512) uint8_t kb0[W::BUFB];
+  __shared__ __align__(512) uint8_t kb1[W::BUFB];
+  __shared__ __align__(512) uint8_t vb0[W::BUFB];
+  __shared__ __align__(512) uint8_t vb1[W::BUFB];
   __shared__ float mlx[2][2][2][64];  // [key half][query block][m, l][lane]
 
   // this workgroup's item list: {first word, count}
@@ -1045,14 +1056,20 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
 
   // Wave-wide load i of this wave fills 1 KiB segment wave + i * WAVES of a buffer: lane t
   // writes bytes 16t.. of it, i.e. key row (wave + i * WAVES) * RPS + t / NCH, slot t % NCH,
-  // which holds chunk slot ^ sw(row) of that row; sw(row) is the same for every i, so load
-  // i's lane offset is load 0's plus i * WAVES * RPS rows. One buffer resource per tile:
-  // base = the tile's first token at the item's KV head, range = the tile's rows inside the
-  // segment (rows past it read as zero; a tile past the item reads nothing), so a step
-  // builds two resources and no per-load scalar arithmetic.
-  const int dma_r0 = wave * W::RPS + lane / W::NCH;
-  const int dma_off = int(dma_r0 * kv_row_b) + (((lane % W::NCH) ^ W::sw(dma_r0)) << 4);
-  const int dma_step = int(W::WAVES * W::RPS * kv_row_b);
+  // which holds chunk slot ^ sw(row) of that row; sw(row) repeats every LOAD_PERIOD loads,
+  // so load i's lane offset is load i % LOAD_PERIOD's plus (i / LOAD_PERIOD) * WAVES * RPS *
+  // LOAD_PERIOD rows. One buffer resource per tile: base = the tile's first token at the
+  // item's KV head, range = the tile's rows inside the segment (rows past it read as zero; a
+  // tile past the item reads nothing), so a step builds two resources and no per-load scalar
+  // arithmetic.
+  constexpr int LP = W::LOAD_PERIOD;
+  int dma_off[LP];
+#pragma unroll
+  for (int p = 0; p < LP; ++p) {
+    const int r = (wave + p * W::WAVES) * W::RPS + lane / W::NCH;
+    dma_off[p] = int(r * kv_row_b) + (((lane % W::NCH) ^ W::sw(r)) << 4);
+  }
+  const int dma_step = int(W::WAVES * W::RPS * LP * kv_row_b);
   auto issue = [&](const char* seg, const Item& it, int t, uint8_t* dst) {
     const int rows = t < it.t_end ? min(it.L - t * BK, BK) : 0;
     const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(seg + int64_t(t) * (BK * kv_row_b)), (short)0,
@@ -1060,7 +1077,7 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
 #pragma unroll
     for (int i = 0; i < LPW; ++i) {
       buffer_load_lds16(rs, (lds_void_t*)((__attribute__((address_space(3))) uint8_t*)dst + (wave + i * W::WAVES) * 1024),
-                        dma_off + i * dma_step);
+                        dma_off[i % LP] + (i / LP) * dma_step);
     }
   };
   // the item's K and V at its segment's first token and its KV head
@@ -1071,16 +1088,20 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
   // along each row, each row loaded once per workgroup), into V buffer 1, which is idle
   // from the end of an item's fold until the next item's second step; rows past the
   // segment read as zero. Its operand reads are the K reads shifted by (qb - kh) x 32 rows
-  // (sw(r) depends on r mod 32 only).
+  // (sw(r) depends on r mod SW_PERIOD, which divides 32, only).
   // The lane offsets are rebuilt per call from an opaque copy of the lane id (kept live
   // through the item loop they would be spilled).
   const int64_t q_row_b = q_row * int64_t(sizeof(T));
   auto issue_q = [&](const Item& it) {
     int ql = lane;
     asm volatile("" : "+v"(ql));
-    const int qr0 = wave * W::RPS + ql / W::NCH;
-    const int qdma_off = int(qr0 * q_row_b) + (((ql % W::NCH) ^ W::sw(qr0)) << 4);
-    const int qdma_step = int(W::WAVES * W::RPS * q_row_b);
+    int qdma_off[LP];
+#pragma unroll
+    for (int p = 0; p < LP; ++p) {
+      const int r = (wave + p * W::WAVES) * W::RPS + ql / W::NCH;
+      qdma_off[p] = int(r * q_row_b) + (((ql % W::NCH) ^ W::sw(r)) << 4);
+    }
+    const int qdma_step = int(W::WAVES * W::RPS * LP * q_row_b);
     const int rows = min(it.L - it.row0, BQ);
     const auto rs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<char*>(reinterpret_cast<const char*>(q) + int64_t(it.seq0 + it.row0) * q_row_b + it.h * ROWB),
@@ -1088,7 +1109,7 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
 #pragma unroll
     for (int i = 0; i < LPW; ++i) {
       buffer_load_lds16(rs, (lds_void_t*)((__attribute__((address_space(3))) uint8_t*)vb1 + (wave + i * W::WAVES) * 1024),
-                        qdma_off + i * qdma_step);
+                        qdma_off[i % LP] + (i / LP) * qdma_step);
     }
   };
   static_assert(BQ == BK, "a Q tile has the layout of a K tile");
@@ -1096,16 +1117,21 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
 
   // LDS byte offsets of this lane's operands within a buffer (as in the ring kernel): K
   // fragment of k-step ks, and the two transposed reads of each V^T operand (the second
-  // 16-key k-step sits 16 rows on, which keeps sw(key), so it is a constant offset).
-  int k_rd[KS];
+  // 16-key k-step sits 16 rows on, which keeps sw(key), so it is a constant offset). At
+  // head_dim 256 they are derived per read from three bases instead of held (32 registers
+  // the lone wave per SIMD cannot spare): chunk (2 ks + g) ^ sw(r) = (g ^ sw(r)) ^ 2 ks, and
+  // chunk (4 db + x) ^ sw(key) = (x ^ sw(key)) ^ 4 db, the k-step and block bits disjoint from
+  // the row bits.
+  constexpr bool kXorOff = D == 256;
+  int k_rd[kXorOff ? 1 : KS];
+  int v_rd[kXorOff ? 1 : DB][2];
   {
     const int r = kh * 32 + col;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) k_rd[ks] = r * ROWB + (((ks * 2 + g) ^ W::sw(r)) << 4);
+    for (int ks = 0; ks < (kXorOff ? 1 : KS); ++ks) k_rd[ks] = r * ROWB + (((ks * 2 + g) ^ W::sw(r)) << 4);
   }
-  int v_rd[DB][2];
 #pragma unroll
-  for (int db = 0; db < DB; ++db) {
+  for (int db = 0; db < (kXorOff ? 1 : DB); ++db) {
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       const int key = kh * 32 + 8 * hh + 4 * g + ((lane & 15) >> 2);
@@ -1113,6 +1139,20 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
       v_rd[db][hh] = key * ROWB + (((d0 >> 3) ^ W::sw(key)) << 4) + ((d0 >> 2) & 1) * 8;
     }
   }
+  static_assert(!kXorOff || (ROWB % 512 == 0 && W::SWB == 4), "XOR offsets: chunk bits 4-8 free of row bits");
+  // (the bases pass through an empty asm at each use site's step: otherwise the compiler
+  // hoists all the XORed offsets out of the loop and spills them)
+  int kx = k_rd[0], vx0 = v_rd[0][0], vx1 = v_rd[0][1];
+  auto fresh_bases = [&]() {
+    if constexpr (kXorOff) {
+      kx = k_rd[0];
+      vx0 = v_rd[0][0];
+      vx1 = v_rd[0][1];
+      asm volatile("" : "+v"(kx), "+v"(vx0), "+v"(vx1));
+    }
+  };
+  auto koff = [&](int ks) { return kXorOff ? (kx ^ (ks << 5)) : k_rd[ks]; };
+  auto voff = [&](int db, int hh) { return kXorOff ? ((hh ? vx1 : vx0) ^ (db << 6)) : v_rd[db][hh]; };
   static_assert(W::sw(16) == W::sw(0) && W::sw(17) == W::sw(1), "16-row shift keeps the swizzle");
 
   // first item: Q, K(t0), K(t0+1) and V(t0) in flight (later items get them from the
@@ -1137,11 +1177,12 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
     floatx16 cur;
     {
       const uint8_t* qbuf = vb1 + (qb - kh) * 32 * ROWB;
+      fresh_bases();
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) qB[ks] = *reinterpret_cast<const uint4*>(qbuf + k_rd[ks]);
+      for (int ks = 0; ks < KS; ++ks) qB[ks] = *reinterpret_cast<const uint4*>(qbuf + koff(ks));
       uint4 kf[KS];
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) kf[ks] = *reinterpret_cast<const uint4*>(kb0 + k_rd[ks]);
+      for (int ks = 0; ks < KS; ++ks) kf[ks] = *reinterpret_cast<const uint4*>(kb0 + koff(ks));
       cur = zero16();
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) cur = mfma32<T>(kf[ks], qB[ks], cur);
@@ -1162,9 +1203,9 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
 #pragma unroll
         for (int t2 = 0; t2 < 2; ++t2) {
           const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_short4_t*)((__attribute__((address_space(3))) const uint8_t*)vb + v_rd[db][0] + t2 * 16 * ROWB));
+              (lds_short4_t*)((__attribute__((address_space(3))) const uint8_t*)vb + voff(db, 0) + t2 * 16 * ROWB));
           const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_short4_t*)((__attribute__((address_space(3))) const uint8_t*)vb + v_rd[db][1] + t2 * 16 * ROWB));
+              (lds_short4_t*)((__attribute__((address_space(3))) const uint8_t*)vb + voff(db, 1) + t2 * 16 * ROWB));
           const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
           vf[db][t2] = make_uint4(l2.x, l2.y, h2.x, h2.y);
         }
@@ -1187,11 +1228,33 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
       // SIMD (one per workgroup) both have work, the one in its MFMA/softmax section issues
       // first, which keeps the matrix pipe fed (3-4% faster than equal priorities).
       __builtin_amdgcn_s_setprio(1);
-      uint4 kf[KS];
+      // At head_dim 256 the K and V^T operands are read and used in NH = 2 parts (k-steps,
+      // head-dim blocks), so that only half of them hold registers at once.
+      constexpr int NH = D == 256 ? 2 : 1;
+      constexpr int KSH = KS / NH, DBH = DB / NH;
+      fresh_bases();
+      uint4 kf[KSH];
+      uint4 vf[DBH][2];
+      auto read_part = [&](int hf) {
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) kf[ks] = *reinterpret_cast<const uint4*>(kb_next + k_rd[ks]);
-      uint4 vf[DB][2];
-      if constexpr (kPV) read_vt(vb_prev, vf);
+        for (int i = 0; i < KSH; ++i) kf[i] = *reinterpret_cast<const uint4*>(kb_next + koff(hf * KSH + i));
+        if constexpr (kPV) {
+#pragma unroll
+          for (int i = 0; i < DBH; ++i) {
+            const int db = hf * DBH + i;
+#pragma unroll
+            for (int t2 = 0; t2 < 2; ++t2) {
+              const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                  (lds_short4_t*)((__attribute__((address_space(3))) const uint8_t*)vb_prev + voff(db, 0) + t2 * 16 * ROWB));
+              const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                  (lds_short4_t*)((__attribute__((address_space(3))) const uint8_t*)vb_prev + voff(db, 1) + t2 * 16 * ROWB));
+              const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+              vf[i][t2] = make_uint4(l2.x, l2.y, h2.x, h2.y);
+            }
+          }
+        }
+      };
+      read_part(0);
       // online softmax of tile t (raw score units, scale folded into the exp2 argument),
       // lazy rescaling as in the ring kernel
       floatx16 sc = cur;
@@ -1233,24 +1296,34 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
       asm volatile("" : "+v"(pN[0].x), "+v"(pN[0].y), "+v"(pN[0].z), "+v"(pN[0].w),
                         "+v"(pN[1].x), "+v"(pN[1].y), "+v"(pN[1].z), "+v"(pN[1].w));
       floatx16 nxt = zero16();
+      auto mfma_part = [&](int hf) {
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) nxt = mfma32<T>(kf[ks], qB[ks], nxt);
-      if constexpr (kPV) {
+        for (int i = 0; i < KSH; ++i) nxt = mfma32<T>(kf[i], qB[hf * KSH + i], nxt);
+        if constexpr (kPV) {
 #pragma unroll
-        for (int db = 0; db < DB; ++db) {
+          for (int i = 0; i < DBH; ++i) {
 #pragma unroll
-          for (int t2 = 0; t2 < 2; ++t2) o[db] = mfma32<T>(vf[db][t2], pB[t2], o[db]);
+            for (int t2 = 0; t2 < 2; ++t2) o[hf * DBH + i] = mfma32<T>(vf[i][t2], pB[t2], o[hf * DBH + i]);
+          }
         }
-      }
-      // K fragments first, softmax work while the reads land, V^T reads, then one MFMA per
-      // group of vector instructions
-      __builtin_amdgcn_sched_group_barrier(0x0100, KS, 0);
-      __builtin_amdgcn_sched_group_barrier(0x0002, 20, 0);
-      if constexpr (kPV) __builtin_amdgcn_sched_group_barrier(0x0100, 4 * DB, 0);
+      };
+      mfma_part(0);
+      if constexpr (NH == 1) {
+        // K fragments first, softmax work while the reads land, V^T reads, then one MFMA per
+        // group of vector instructions
+        __builtin_amdgcn_sched_group_barrier(0x0100, KS, 0);
+        __builtin_amdgcn_sched_group_barrier(0x0002, 20, 0);
+        if constexpr (kPV) __builtin_amdgcn_sched_group_barrier(0x0100, 4 * DB, 0);
 #pragma unroll
-      for (int i = 0; i < (kPV ? 2 : 1) * KS; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x0002, kPV ? 5 : 9, 0);
+        for (int i = 0; i < (kPV ? 2 : 1) * KS; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x0002, kPV ? 5 : 9, 0);
+        }
+      } else {
+        // the second half's reads go out behind the first half's MFMAs
+        __builtin_amdgcn_sched_barrier(0);
+        read_part(1);
+        mfma_part(1);
       }
       // O (with PV(t-1) added) moves to tile t's reference max
       if (moved) {
@@ -1275,6 +1348,7 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
     if (sidx < n_it) step(sidx, kb0, kb1, vb0, vb1, PV{});
     // PV of the last tile, whose V landed in buffer (n_it - 1) & 1
     auto drain = [&](const uint8_t* vb) {
+      fresh_bases();
       uint4 vf[DB][2];
       read_vt(vb, vf);
 #pragma unroll
@@ -1350,19 +1424,27 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
       // K and V that the following items re-read.
       constexpr int NC = HB * 4;  // 16-byte chunks of a staged row
       uint8_t* stg = fbuf_bytes + KH * HB * 16 * 64 * 4;
+      // every kept block is combined before any is staged: the staging area overlaps the
+      // blocks (from the second one on, when a wave keeps more than two)
+      float r[HB][16];
 #pragma unroll
       for (int hb = 0; hb < HB; ++hb) {
         const int db = KH * HB + hb;
-        float r[16];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) r[e] = fmaf(fbuf[(db * 16 + e) * 64 + ln], w_o, o[db][e] * w_me);
+        for (int e = 0; e < 16; ++e) r[hb][e] = fmaf(fbuf[(db * 16 + e) * 64 + ln], w_o, o[db][e] * w_me);
+      }
+#pragma unroll
+      for (int hb = 0; hb < HB; ++hb) {
+        const int db = KH * HB + hb;
         if (cur_it.n_split <= 1) {
 #pragma unroll
           for (int jg = 0; jg < 4; ++jg) {
-            const uint2 val = make_uint2(pack2<T>(r[jg * 4 + 0] * inv, r[jg * 4 + 1] * inv),
-                                         pack2<T>(r[jg * 4 + 2] * inv, r[jg * 4 + 3] * inv));
+            // written as floats: the same bytes, in a type the compiler's LDS alias tracking
+            // keeps apart from the next item's K loads in flight (it would wait for them)
             const int pos = (hb * 4 + jg) ^ (e_col & (NC - 1));
-            *reinterpret_cast<uint2*>(stg + e_col * (NC * 16) + pos * 16 + e_g * 8) = val;
+            float* f = fbuf + (KH * HB * 16 * 64 * 4 + e_col * (NC * 16) + pos * 16 + e_g * 8) / 4;
+            f[0] = __builtin_bit_cast(float, pack2<T>(r[hb][jg * 4 + 0] * inv, r[hb][jg * 4 + 1] * inv));
+            f[1] = __builtin_bit_cast(float, pack2<T>(r[hb][jg * 4 + 2] * inv, r[hb][jg * 4 + 3] * inv));
           }
         } else {
           // this piece's (O relative to M, M, l) for the merge launch; rows past the segment
@@ -1373,7 +1455,7 @@ __global__ __launch_bounds__(Duo<D>::THREADS, 2) void varlen_prefill_duo_kernel(
           for (int jg = 0; jg < 4; ++jg) {
             const int d = db * 32 + jg * 8 + e_g * 4;
             *reinterpret_cast<float4*>(pbase + row * D + d) =
-                make_float4(r[jg * 4 + 0], r[jg * 4 + 1], r[jg * 4 + 2], r[jg * 4 + 3]);
+                make_float4(r[hb][jg * 4 + 0], r[hb][jg * 4 + 1], r[hb][jg * 4 + 2], r[hb][jg * 4 + 3]);
           }
           if (KH == 0 && hb == 0 && e_g == 0) *reinterpret_cast<float2*>(pbase + BQ * D + row * 2) = make_float2(M, l_all);
         }
@@ -1487,7 +1569,9 @@ int kind_rows(int kind) {
 // keys per schedule unit of work (a causal tile's cost is counted in these)
 int kind_keys(int kind) { return kind == kDuo ? Duo<128>::BK : Ring<128>::BK; }
 // workgroups one CU holds at once
-int kind_per_cu(int kind) { return kind == kDuo || kind == kStaged ? 2 : 1; }
+int kind_per_cu(int kind, int D) {
+  return kind == kDuo ? (D == 256 ? Duo<256>::PER_CU : Duo<128>::PER_CU) : kind == kStaged ? 2 : 1;
+}
 static_assert(Ring<128>::BK == Tiles<256>::BK && Ring<64>::BK == Tiles<128>::BK, "64-key tiles");
 static_assert(Duo<64>::BQ == Duo<128>::BQ && Duo<64>::BK == Duo<128>::BK, "duo tile shape");
 
@@ -1496,17 +1580,19 @@ int launch2(const void* q, const void* k, const void* v, void* out, const int32_
             const int32_t* sched, int n_work, int n_merge, int kind, float* partials, int H,
             int H_kv, float scale_log2, int causal, hipStream_t s) {
   const int32_t* work = sched + kSchedHeader;
-  if constexpr (D == 64 || D == 128) {
-    if (kind == kRing || kind == kDuo) {
+  if constexpr (D == 64 || D == 128 || D == 256) {
+    if (kind == kDuo || (D != 256 && kind == kRing)) {
       constexpr int kRowsPerBlock = 256 / (D / 32);
       if (kind == kRing) {
-        hipLaunchKernelGGL((varlen_prefill_ring_kernel<T, D>), dim3(H, n_work), dim3(Ring<D>::THREADS), 0, s,
-                           static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
-                           static_cast<T*>(out), cu, work, partials, H, H_kv, H / H_kv, scale_log2, causal);
-        if (n_merge > 0) {
-          hipLaunchKernelGGL((varlen_prefill_merge_kernel<T, D, Ring<D>::BQ>),
-                             dim3(H, n_merge, (Ring<D>::BQ + kRowsPerBlock - 1) / kRowsPerBlock), dim3(256), 0, s,
-                             cu, work + 2 * n_work, static_cast<const float*>(partials), static_cast<T*>(out), H);
+        if constexpr (D != 256) {
+          hipLaunchKernelGGL((varlen_prefill_ring_kernel<T, D>), dim3(H, n_work), dim3(Ring<D>::THREADS), 0, s,
+                             static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
+                             static_cast<T*>(out), cu, work, partials, H, H_kv, H / H_kv, scale_log2, causal);
+          if (n_merge > 0) {
+            hipLaunchKernelGGL((varlen_prefill_merge_kernel<T, D, Ring<D>::BQ>),
+                               dim3(H, n_merge, (Ring<D>::BQ + kRowsPerBlock - 1) / kRowsPerBlock), dim3(256), 0, s,
+                               cu, work + 2 * n_work, static_cast<const float*>(partials), static_cast<T*>(out), H);
+          }
         }
       } else if (kind == kDuo) {
         // n_work persistent workgroups; their item table follows the header, the merge
@@ -1559,7 +1645,8 @@ struct Piece { int work, w0, w1; };
 // 3, 31.8 with 12, 32.9 with 16; batches of equal or mid-length segments unchanged).
 int duo_schedule(const int32_t* cu, const std::vector<Piece>& pieces, const std::vector<Piece>& merges,
                  int n_partials, int H, int H_kv, int D, int32_t* out, int capacity) {
-  constexpr int kCUs = 256, kSlots = 2 * kCUs, kItemOverhead = 8;
+  constexpr int kCUs = 256, kItemOverhead = 8;
+  const int kSlots = kCUs * kind_per_cu(kDuo, D);
   const int64_t n_items = int64_t(pieces.size()) * H;
   const int n_wg = int(std::min<int64_t>(kSlots, n_items));
   const int n_merge = int(merges.size());
@@ -1632,9 +1719,11 @@ extern "C" int mi_varlen_schedule_for(const int32_t* host_cu_seqlens, int n_seqs
   if (kernel < MI_PREFILL_AUTO || kernel > MI_PREFILL_DUO || kernel == 2) {
     return fail(MI_ERR_INVALID, "mi_varlen_schedule: unknown prefill kernel %d", kernel);
   }
-  if (kernel != MI_PREFILL_AUTO && kernel != MI_PREFILL_STAGED && D != 64 && D != 128) {
-    return fail(MI_ERR_UNSUPPORTED, "mi_varlen_schedule: the ring and duo kernels take head_dim 64 or 128, got %d",
-                D);
+  if (kernel == MI_PREFILL_RING && D != 64 && D != 128) {
+    return fail(MI_ERR_UNSUPPORTED, "mi_varlen_schedule: the ring kernel takes head_dim 64 or 128, got %d", D);
+  }
+  if (kernel == MI_PREFILL_DUO && D != 64 && D != 128 && D != 256) {
+    return fail(MI_ERR_UNSUPPORTED, "mi_varlen_schedule: the duo kernel takes head_dim 64, 128 or 256, got %d", D);
   }
   if (host_cu_seqlens == nullptr || n_seqs < 1 || n_seqs > 65535) {
     return fail(MI_ERR_INVALID, "mi_varlen_schedule: need 1..65535 segments, got %d", n_seqs);
@@ -1653,7 +1742,7 @@ extern "C" int mi_varlen_schedule_for(const int32_t* host_cu_seqlens, int n_seqs
   // register-staged kernel); the caller may name a kernel instead.
   const int kind = kernel == MI_PREFILL_STAGED ? kStaged : kernel == MI_PREFILL_RING ? kRing
                  : kernel == MI_PREFILL_DUO ? kDuo
-                 : (D == 64 || D == 128) ? (max_len >= kRingMinLen ? kRing : kDuo) : kStaged;
+                 : (D == 64 || D == 128) ? (max_len >= kRingMinLen ? kRing : kDuo) : D == 256 ? kDuo : kStaged;
   const bool ring = kind != kStaged;  // one workgroup per CU, split-K capable
   const int RW = kind_rows(kind);
   const int BN = kind_keys(kind);
@@ -1679,7 +1768,7 @@ extern "C" int mi_varlen_schedule_for(const int32_t* host_cu_seqlens, int n_seqs
   // the chip is not split: its pieces would only add per-workgroup start-up and merge
   // cost (measured slower on the config-3 batch, 46 + 8 us against 42 us unsplit).
   constexpr int kCUs = 256, kMinPiece = 8;
-  const int slots = kCUs * kind_per_cu(kind);  // workgroups the chip runs at once
+  const int slots = kCUs * kind_per_cu(kind, D);  // workgroups the chip runs at once
   const int64_t share = (total * H + slots - 1) / slots;
   const bool underfilled = int64_t(tiles.size()) * H < slots;
   const int cap = underfilled ? int(std::max<int64_t>(share, kMinPiece)) : INT32_MAX;
@@ -1762,7 +1851,8 @@ extern "C" int mi_varlen_prefill(const void* q, const void* k, const void* v, vo
   const int kind = layout_kind(layout);
   const bool split_capable = kind == kRing || kind == kDuo;
   if (layout_d(layout) != D || kind < kStaged || kind > kDuo || kind == 2 || rows != kind_rows(kind) ||
-      (split_capable && D != 64 && D != 128) || (n_merge > 0) != (n_partials > 0) ||
+      (kind == kRing && D != 64 && D != 128) || (kind == kDuo && D != 64 && D != 128 && D != 256) ||
+      (n_merge > 0) != (n_partials > 0) ||
       (n_merge > 0 && !split_capable)) {
     return fail(MI_ERR_INVALID, "mi_varlen_prefill: schedule (layout 0x%x) does not match head_dim %d",
                 layout, D);

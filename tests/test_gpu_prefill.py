@@ -67,7 +67,7 @@ def test_matches_the_per_segment_oracle(lengths, H, H_kv, kernel, cuda):
 
 @pytest.mark.parametrize("D,kernel", [(64, None), (64, "ring"), (64, "staged"), (64, "duo"),
                                       (128, None), (128, "ring"), (128, "staged"), (128, "duo"),
-                                      (256, None)])
+                                      (256, None), (256, "staged"), (256, "duo")])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 def test_head_dims_and_dtypes(D, kernel, dtype, cuda):
     q, k, v, cu, ms = _packed([1, 33, 128, 300], 8, 4, D, dtype=dtype, seed=2)
@@ -159,6 +159,19 @@ def test_config3_full_size(kernel, dtype, cuda):
     assert excess <= PREFILL_EXCESS_BAR[dtype]
 
 
+@pytest.mark.parametrize("kernel", [pytest.param(None, id="default"), pytest.param("staged", id="staged")])
+def test_config3_qwen35_shape(kernel, cuda):
+    """Config 3's lengths at the Qwen3.5 attention shape (H 8 / H_kv 2 / head_dim 256): the
+    default choice there is the duo kernel at one workgroup per CU; the register-staged
+    kernel is the other that takes head_dim 256."""
+    inp = W.prefill_config3(H=8, H_kv=2, D=256)
+    out = _run(inp.q, inp.k, inp.v, inp.cu_seqlens, max(inp.lengths), cuda, kernel).float()
+    ref = longhand_varlen(inp.q, inp.k, inp.v, inp.cu_seqlens)
+    assert (out - ref).abs().max().item() <= 2e-2
+    excess = ((out - ref).abs() - ref.abs() * OUTPUT_ULP[torch.bfloat16]).max().item()
+    assert excess <= PREFILL_EXCESS_BAR[torch.bfloat16]
+
+
 def test_error_surface(cuda):
     q, k, v, cu, ms = _packed([4, 4], 8, 4, 128, dtype=torch.float32)
     with pytest.raises(RuntimeError, match="fp16/bf16"):
@@ -175,7 +188,7 @@ def test_error_surface(cuda):
     with pytest.raises(ValueError, match="head_dim 64 or 128"):
         q256 = torch.zeros(8, 8, 256, dtype=torch.bfloat16, device=cuda)
         k256 = torch.zeros(8, 4, 256, dtype=torch.bfloat16, device=cuda)
-        HipVarlen("duo").prefill_varlen(q256, k256, k256, cu_seqlens=[0, 8], max_seqlen=8)
+        HipVarlen("ring").prefill_varlen(q256, k256, k256, cu_seqlens=[0, 8], max_seqlen=8)
     assert backend_for("cuda").name == "hip-mfma-varlen"
     assert isinstance(backend_for(torch.device("cuda:0")), HipVarlen)
 
