@@ -10,8 +10,9 @@ than Python launch overhead; the eager (un-captured) step time is reported besid
 Algorithmic bytes per layer = sum(seqlen) * 2 * H_kv * D * 2 B (K and V read once per KV
 head) + q and out (2 * B * H * D * 2 B) + seqlen + block table.
 
-Extra fields: packed prefill (config 3) TFLOP/s against bf16 MFMA peak, the packed KV
-slot write (config 3) GB/s, long-context split-K decode (config 4), and the CPU baseline:
+Extra fields: packed prefill (config 3) TFLOP/s against bf16 MFMA peak, also at the
+Qwen3.5 attention shape (H 8 / H_kv 2 / head_dim 256), the packed KV slot write (config
+3) GB/s, long-context split-K decode (config 4), and the CPU baseline:
 the reference's seat path (contiguous slab + baddbmm decode, bf16 softmax) timed on this
 host's cores on one layer of the same config-2 inputs, after checking the GPU output
 against it.
@@ -379,6 +380,51 @@ def copy_calibration(mib: int, reps: int) -> dict:
             "gbs_read_plus_write": 2 * n * 2 / dt / 1e9}
 
 
+def bench_prefill_qwen35(stream, steps: int = 20, eager: bool = False) -> dict:
+    """Config 3's lengths at the Qwen3.5 attention shape (H 8 / H_kv 2 / head_dim 256): the
+    packed prefill (28 layer calls on one packed group, HIP-graph replay), checked against
+    the fp32 longhand oracle before it is timed."""
+    from miattn import HipVarlen
+    from miattn import workloads as W
+
+    from oracle.varlen import longhand_varlen
+
+    inp = W.prefill_config3(device="cuda", H=8, H_kv=2, D=256)
+    backend = HipVarlen()
+    H, D = inp.q.shape[1], inp.q.shape[2]
+    flop = 4 * H * D * sum(n * (n + 1) // 2 for n in inp.lengths)
+    ms = max(inp.lengths)
+    got = backend.prefill_varlen(inp.q, inp.k, inp.v, cu_seqlens=inp.cu_seqlens, max_seqlen=ms).cpu().float()
+    diff = (got - longhand_varlen(inp.q.cpu(), inp.k.cpu(), inp.v.cpu(), inp.cu_seqlens)).abs().max().item()
+    if not diff <= 2e-2:
+        raise SystemExit(f"Qwen3.5-shape prefill disagrees with the oracle: max|delta|={diff}")
+
+    def prefill_step():
+        for _ in range(N_LAYER):
+            backend.prefill_varlen(inp.q, inp.k, inp.v, cu_seqlens=inp.cu_seqlens, max_seqlen=ms)
+
+    if eager:  # plain dispatches, for counter collection
+        with torch.cuda.stream(stream):
+            for _ in range(2):
+                prefill_step()
+            torch.cuda.synchronize()
+            with EventTimer(stream) as t:
+                prefill_step()
+            step_ms = t.ms()
+    else:
+        step_ms, _ = time_graph(prefill_step, stream, steps, 3)
+    us = step_ms / N_LAYER * 1e3
+    tflops = flop / (us * 1e-6) / 1e12
+    return {
+        "workload": "config3 lengths at H8/H_kv2/D256 bf16 (Qwen3.5 attention), 28 layer calls, HIP-graph replay",
+        "prefill_us_per_layer": us,
+        "prefill_tflops": tflops,
+        "prefill_frac_mfma_peak": tflops / BF16_MFMA_PEAK_TFLOPS,
+        "flop_per_layer": flop,
+        "checked": {"max_abs_diff_vs_fp32_oracle": diff},
+    }
+
+
 def bench_block32(stream, steps: int = 50) -> dict:
     """Config 2 with 32-token blocks (the reference's other contract block size): the same
     lengths and the same bytes in 4096 blocks of 32 per layer, checked then timed like the
@@ -577,7 +623,9 @@ def main() -> int:
         print(json.dumps({"e2e": bench_tpot(stream), "config5_trace": bench_config5(stream)}), flush=True)
         return 0
     if args.prefill_only:
-        print(json.dumps({"prefill": bench_prefill(stream, args.steps, eager=args.eager)}), flush=True)
+        print(json.dumps({"prefill": bench_prefill(stream, args.steps, eager=args.eager),
+                          "prefill_qwen35": bench_prefill_qwen35(stream, args.steps, eager=args.eager)}),
+              flush=True)
         return 0
     log("building config-2 inputs (28 layers, 8192 blocks each)")
     inp = W.paged_decode_config(device="cuda", max_blocks=128)
@@ -627,6 +675,8 @@ def main() -> int:
         line["prefill"] = bench_prefill(stream)
         log(f"prefill: {line['prefill']['prefill_tflops']:.1f} TFLOP/s, "
             f"slot write {line['prefill']['slot_write_gbs']:.1f} GB/s")
+        line["prefill_qwen35"] = bench_prefill_qwen35(stream)
+        log(f"prefill (Qwen3.5 shape, D256): {line['prefill_qwen35']['prefill_tflops']:.1f} TFLOP/s")
         log("end-to-end TPOT (config 5 shape, B=32 ctx 2048)")
         line["e2e"] = bench_tpot(stream)
         line["tpot_ms"] = round(line["e2e"]["tpot_ms"], 4)

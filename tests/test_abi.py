@@ -51,10 +51,10 @@ PER_CU = {0: 2, 1: 1, 3: 2}     # workgroups one CU runs at once
 
 
 def _kind(kernel, D, lengths=()):
-    if kernel is None:  # head_dim 64/128: ring from an 8192-token segment, duo below; staged otherwise
+    if kernel is None:  # head_dim 64/128: ring from an 8192-token segment, duo below; 256: duo
         if D in (64, 128):
             return 1 if max(lengths) >= 8192 else 3
-        return 0
+        return 3 if D == 256 else 0
     return KERNELS[kernel]
 
 
@@ -197,10 +197,17 @@ def test_schedule_splits_only_launches_that_underfill_the_chip(kernel, H):
         assert not merges and all(p[3] == 1 for p in pieces)
 
 
-def test_schedule_head_dim_256_uses_64_row_tiles_and_never_splits():
+def test_schedule_head_dim_256_runs_the_duo_kernel_one_workgroup_per_cu():
+    """head_dim 256 defaults to the duo kernel with one persistent workgroup per CU (256 at
+    most); a launch that fills them is not split."""
     lengths = [100, 1700]
     (_, n_merge, n_partials), pieces, _ = _schedule(lengths, D=256)
     assert n_merge == 0 and n_partials == 0
+    host_cu = (ctypes.c_int32 * 3)(0, 100, 1800)
+    words = _lib.lib.mi_varlen_schedule_for(host_cu, 2, 16, 8, 256, 1, -1, None, 0)
+    out = (ctypes.c_int32 * words)()
+    assert _lib.lib.mi_varlen_schedule_for(host_cu, 2, 16, 8, 256, 1, -1, out, words) == words
+    assert out[0] == 256 and out[3] == (3 << 20) | (256 << 8) | 64  # workgroups, duo layout
     assert sorted((s, t) for s, t, *_ in pieces) == sorted(
         {(s, t) for s, n in enumerate(lengths) for t in range(-(-n // 64))})
 
@@ -212,6 +219,8 @@ def test_schedule_rejects_unknown_kernels_and_head_dims():
     assert _lib.lib.mi_varlen_schedule_for(host_cu, 1, 16, 8, 128, 1, 2, None, 0) == _lib.MI_ERR_INVALID  # removed
     assert _lib.lib.mi_varlen_schedule_for(host_cu, 1, 16, 8, 256, 1, 1, None, 0) == _lib.MI_ERR_UNSUPPORTED
     assert _lib.lib.mi_varlen_schedule_for(host_cu, 1, 16, 8, 256, 1, 0, None, 0) > 0
+    assert _lib.lib.mi_varlen_schedule_for(host_cu, 1, 16, 8, 256, 1, 3, None, 0) > 0
+    assert _lib.lib.mi_varlen_schedule_for(host_cu, 1, 16, 8, 512, 1, 3, None, 0) == _lib.MI_ERR_UNSUPPORTED
 
 
 def test_schedule_rejects_empty_segments():
