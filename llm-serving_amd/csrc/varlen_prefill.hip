@@ -527,7 +527,11 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
 // Workgroup barrier without the release/acquire fences of __syncthreads: those would wait
 // for every LDS-bound load in flight, including the tile two steps ahead. The waits that
 // matter are explicit (wait_vm_lgkm0) and the memory clobber keeps LDS accesses on their
-// side of the barrier.
+// side of the barrier. Every wave loads a share of each tile (counted in vmcnt only), so
+// at each barrier of the ring and duo kernels: (1) a tile read after it was waited for, by
+// every wave, for that wave's own loads of it (vmcnt(N), N = loads issued after them; they
+// retire in order); (2) a buffer refilled after it is no longer read by any wave before
+// it (lgkmcnt(0) in the same wait).
 __device__ __forceinline__ void bare_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 template <typename T, int D>
