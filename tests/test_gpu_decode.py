@@ -312,6 +312,24 @@ def test_duplicated_blocks_and_an_unread_table_tail(dtype, D, cuda):
     assert (got.float() - expected).abs().max().item() < tol
 
 
+@pytest.mark.parametrize("B,seed", [(100, 61), (130, 62)])
+def test_batches_past_64_rows(B, seed, cuda):
+    """The device plan scans the row lengths 64 rows per wave pass and carries the split
+    count across passes: 100 and 130 ragged rows, zero-length rows in every pass, against
+    the fp32 gather oracle."""
+    gen = torch.Generator().manual_seed(seed)
+    lengths = torch.randint(1, 400, (B,), generator=gen).tolist()
+    for row in (0, 63, 64, B - 1):
+        lengths[row] = 0
+    lengths[65] = 1
+    q, k, v, table, seqlen = _build(B, 16, 8, 128, 16, lengths, dtype=torch.bfloat16, seed=seed)
+    got = paged_decode(q, k, v, table, seqlen)
+    torch.cuda.synchronize()
+    expected = reference_paged_decode(*_cpu(q, k, v, table, seqlen), out_dtype=torch.float32)
+    assert (got.cpu().float() - expected).abs().max().item() < 2e-2
+    assert not got[[0, 63, 64, B - 1]].any()
+
+
 def test_zero_length_rows_next_to_long_rows(cuda):
     """Rows of length 0 (exact zeros, reference :352-365) between split-K rows."""
     lengths = [0, 5000, 0, 1, 3000, 0]

@@ -94,6 +94,29 @@ def test_long_segments_and_split_pieces(lengths, H, H_kv, D, dtype, kernel, cuda
     assert (out.float() - longhand_varlen(q, k, v, cu)).abs().max().item() <= 2e-2
 
 
+@pytest.mark.parametrize("kernel", [pytest.param(None, id="default"), pytest.param("duo", id="duo"),
+                                    pytest.param("staged", id="staged")])
+@pytest.mark.parametrize("lengths", [pytest.param([1500], id="split-1500"), pytest.param([900, 3], id="split-900")])
+def test_head_dim_256_split_pieces(lengths, kernel, cuda):
+    """Head_dim 256 on a launch too small to fill the chip (H 8 / H_kv 2): the schedule
+    splits the longest tiles' key ranges and the merge launch folds the pieces."""
+    q, k, v, cu, ms = _packed(lengths, 8, 2, 256, seed=13)
+    out = _run(q, k, v, cu, ms, cuda, kernel)
+    assert torch.isfinite(out).all()
+    assert (out.float() - longhand_varlen(q, k, v, cu)).abs().max().item() <= 2e-2
+
+
+@pytest.mark.parametrize("kernel", KERNELS)
+def test_many_short_segments(kernel, cuda):
+    """150 short segments (1-89 tokens) in one pack: every tile of every segment gets its
+    own schedule entry, and no query sees another segment's keys."""
+    gen = torch.Generator().manual_seed(71)
+    lengths = torch.randint(1, 90, (150,), generator=gen).tolist()
+    q, k, v, cu, ms = _packed(lengths, 8, 4, 128, seed=11)
+    out = _run(q, k, v, cu, ms, cuda, kernel)
+    assert (out.float() - longhand_varlen(q, k, v, cu)).abs().max().item() <= 2e-2
+
+
 @pytest.mark.parametrize("kernel", KERNELS)
 def test_long_non_causal(kernel, cuda):
     q, k, v, cu, ms = _packed([2050, 70], 8, 4, 128, seed=8)
