@@ -250,8 +250,10 @@ int mi_paged_decode_noalloc(const void* q, const void* k_cache, const void* v_ca
  * tiles. By default head_dim 64/128 batches whose longest segment reaches 8192 tokens run
  * the LDS-ring kernel (128-row tiles), shorter ones the persistent duo kernel (64-row
  * tiles, two workgroups per CU, each working through its own item list), head_dim 256 the
- * duo kernel at one workgroup per CU; mi_varlen_schedule_for names the kernel instead
- * (MI_PREFILL_*; the ring kernel takes head_dim 64 and 128, the duo kernel 64, 128 and 256,
+ * duo kernel at one workgroup per CU; batches of more than 255 heads (beyond the duo
+ * kernel's item word) run the ring kernel at head_dim 64/128 and the register-staged
+ * kernel at 256. mi_varlen_schedule_for names the kernel instead (MI_PREFILL_*; the ring
+ * kernel takes head_dim 64 and 128, the duo kernel 64, 128 and 256 with at most 255 heads,
  * the register-staged kernel all three). Layout of
  * the staged and ring schedules:
  * {n_work, n_merge, n_partials, layout}, then n_work work entries and n_merge merge

@@ -1742,11 +1742,15 @@ extern "C" int mi_varlen_schedule_for(const int32_t* host_cu_seqlens, int n_seqs
     return fail(MI_ERR_UNSUPPORTED, "mi_varlen_schedule: the duo kernel takes at most 255 heads, got %d", H);
   }
   // By default head_dim 64 and 128 run the ring kernel when the longest segment reaches
-  // kRingMinLen tokens and the persistent duo kernel otherwise (head_dim 256 runs the
-  // register-staged kernel); the caller may name a kernel instead.
+  // kRingMinLen tokens and the persistent duo kernel otherwise, and head_dim 256 runs the
+  // duo kernel; a batch of more heads than the duo kernel's item word holds (255) runs the
+  // ring kernel (64, 128) or the register-staged kernel (256). The caller may name a kernel
+  // instead.
+  const bool duo_heads = H <= 255;
   const int kind = kernel == MI_PREFILL_STAGED ? kStaged : kernel == MI_PREFILL_RING ? kRing
                  : kernel == MI_PREFILL_DUO ? kDuo
-                 : (D == 64 || D == 128) ? (max_len >= kRingMinLen ? kRing : kDuo) : D == 256 ? kDuo : kStaged;
+                 : (D == 64 || D == 128) ? (max_len >= kRingMinLen || !duo_heads ? kRing : kDuo)
+                 : D == 256 && duo_heads ? kDuo : kStaged;
   const bool ring = kind != kStaged;  // one workgroup per CU, split-K capable
   const int RW = kind_rows(kind);
   const int BN = kind_keys(kind);

@@ -212,6 +212,24 @@ def test_schedule_head_dim_256_runs_the_duo_kernel_one_workgroup_per_cu():
         {(s, t) for s, n in enumerate(lengths) for t in range(-(-n // 64))})
 
 
+def test_schedule_default_leaves_the_duo_kernel_past_255_heads():
+    """The duo item word holds a head id in 8 bits: by default a batch of 256 or more heads
+    runs the ring kernel at head_dim 64/128 and the register-staged kernel at 256, and naming
+    the duo kernel for it is refused."""
+    host_cu = (ctypes.c_int32 * 3)(0, 100, 400)
+
+    def kind(H, H_kv, D, kernel=-1):
+        words = _lib.lib.mi_varlen_schedule_for(host_cu, 2, H, H_kv, D, 1, kernel, None, 0)
+        assert words > 0
+        out = (ctypes.c_int32 * words)()
+        assert _lib.lib.mi_varlen_schedule_for(host_cu, 2, H, H_kv, D, 1, kernel, out, words) == words
+        return out[3] >> 20
+
+    assert kind(255, 5, 128) == 3 and kind(256, 8, 128) == 1 and kind(256, 8, 64) == 1
+    assert kind(255, 5, 256) == 3 and kind(256, 8, 256) == 0
+    assert _lib.lib.mi_varlen_schedule_for(host_cu, 2, 256, 8, 128, 1, 3, None, 0) == _lib.MI_ERR_UNSUPPORTED
+
+
 def test_schedule_rejects_unknown_kernels_and_head_dims():
     host_cu = (ctypes.c_int32 * 2)(0, 5)
     assert _lib.lib.mi_varlen_schedule_for(host_cu, 1, 16, 8, 128, 1, 7, None, 0) == _lib.MI_ERR_INVALID

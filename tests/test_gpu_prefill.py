@@ -106,6 +106,15 @@ def test_head_dim_256_split_pieces(lengths, kernel, cuda):
     assert (out.float() - longhand_varlen(q, k, v, cu)).abs().max().item() <= 2e-2
 
 
+@pytest.mark.parametrize("D", [128, 256])
+def test_default_kernel_past_255_heads(D, cuda):
+    """256 query heads (beyond the duo kernel's item word): the default schedule runs the
+    ring kernel at head_dim 128 and the register-staged kernel at 256."""
+    q, k, v, cu, ms = _packed([70, 5, 130], 256, 8, D, seed=17)
+    out = _run(q, k, v, cu, ms, cuda)
+    assert (out.float() - longhand_varlen(q, k, v, cu)).abs().max().item() <= 2e-2
+
+
 @pytest.mark.parametrize("kernel", KERNELS)
 def test_many_short_segments(kernel, cuda):
     """150 short segments (1-89 tokens) in one pack: every tile of every segment gets its
