@@ -12,7 +12,8 @@
 // that follows reads the source rows, but a packed group's K/V (17.7 MB at 4311 tokens, 35 MB
 // read and written) is far more than one XCD's 4 MB L2 (measured on that group: 10.06 -> 9.30 us, the prefill
 // after it unchanged; more chunks per thread, 2/4/8 with all loads first, measured slower:
-// 10.2/10.6/11.7 us).
+// 10.2/10.6/11.7 us). The row loads do not wait for the slot id (one round trip per chunk,
+// not two: 9.4 -> 8.7-9.0 us).
 // Sources with a non-unit element stride or 16-byte misalignment take the scalar kernel
 // (same bytes, element granularity).
 #include "common.h"
@@ -42,15 +43,20 @@ __global__ __launch_bounds__(256) void slot_write_vec16(
   for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += stride) {
     const int64_t token = i / chunks_per_row;
     const int chunk = int(i - token * chunks_per_row);
-    const IdxT slot = slots[token];
+    const int head = chunk / chunks_per_head;
+    const int part = chunk - head * chunks_per_head;
+    // the source rows do not depend on the slot: their loads go out with the slot id's, so
+    // the chain is one memory round trip, not two
+    uint4 kv = load16_nt(k + token * ks0 + head * ks1 + part * 16);
+    uint4 vv = load16_nt(v + token * vs0 + head * vs1 + part * 16);
+    IdxT slot = slots[token];
+    // (pinned here: left alone the compiler sinks the row loads behind the slot check)
+    asm volatile("" : "+v"(kv.x), "+v"(kv.y), "+v"(kv.z), "+v"(kv.w), "+v"(vv.x), "+v"(vv.y), "+v"(vv.z),
+                      "+v"(vv.w), "+v"(slot));
     if (!slot_in_range(slot, n_slots)) {
       record_bad_token(err, token);
       continue;
     }
-    const int head = chunk / chunks_per_head;
-    const int part = chunk - head * chunks_per_head;
-    const uint4 kv = load16_nt(k + token * ks0 + head * ks1 + part * 16);
-    const uint4 vv = load16_nt(v + token * vs0 + head * vs1 + part * 16);
     const int64_t dst = (int64_t(slot) * chunks_per_row + chunk) * 16;
     store16_nt(k_pool + dst, kv);
     store16_nt(v_pool + dst, vv);
