@@ -162,14 +162,17 @@ __device__ __forceinline__ int split_chunk(int total, int batch, int target) {
   return chunk > batch ? chunk : batch;
 }
 
-// Inclusive prefix sum over the 64 lanes of a wave.
+// Inclusive prefix sum over the 64 lanes of a wave, in DPP moves (no LDS round trips):
+// shifts by 1, 2, 4 and 8 inside each row of 16 lanes (lanes shifted in from outside the
+// row read 0), then lane 15 of rows 0 and 2 added into rows 1 and 3, and lane 31 into rows
+// 2 and 3.
 __device__ __forceinline__ int wave_inclusive_scan(int v) {
-  const int lane = __lane_id();
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int up = __shfl_up(v, off, 64);
-    if (lane >= off) v += up;
-  }
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true);   // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true);   // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true);   // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true);   // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15 -> rows 1, 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31 -> rows 2, 3
   return v;
 }
 
@@ -178,13 +181,16 @@ __device__ __forceinline__ int wave_inclusive_scan(int v) {
 // its own from the row lengths (same inputs, same answer), so planning needs no LDS and no
 // barrier; rows are taken 64 at a time, one per lane.
 struct SplitInfo {
-  int b, split, n_split, first, chunk;
+  int b, split, n_split, first, chunk, len;
 };
 __device__ __forceinline__ bool plan_split(const int32_t* __restrict__ seqlen, int B, int capacity,
                                            int batch, int target, int w, SplitInfo& si) {
   const int lane = __lane_id();
-  int total = 0;
-  for (int r0 = 0; r0 < B; r0 += 64) {
+  // the first 64 rows' lengths are loaded once and serve both passes (one round trip for
+  // batches of up to 64 rows)
+  const int len_first = lane < B ? clamp_len(seqlen[lane], capacity) : 0;
+  int total = __builtin_amdgcn_readlane(wave_inclusive_scan(len_first), 63);
+  for (int r0 = 64; r0 < B; r0 += 64) {
     const int row = r0 + lane;
     const int len = row < B ? clamp_len(seqlen[row], capacity) : 0;
     total += __builtin_amdgcn_readlane(wave_inclusive_scan(len), 63);
@@ -193,7 +199,8 @@ __device__ __forceinline__ bool plan_split(const int32_t* __restrict__ seqlen, i
   int base = 0;  // splits of the rows before this block of 64
   for (int r0 = 0; r0 < B; r0 += 64) {
     const int row = r0 + lane;
-    const int n = row < B ? (clamp_len(seqlen[row], capacity) + chunk - 1) / chunk : 0;
+    const int len = r0 == 0 ? len_first : row < B ? clamp_len(seqlen[row], capacity) : 0;
+    const int n = (len + chunk - 1) / chunk;
     const int incl = wave_inclusive_scan(n);
     const uint64_t owner = __ballot(w >= base + incl - n && w < base + incl);
     if (owner != 0) {
@@ -204,6 +211,7 @@ __device__ __forceinline__ bool plan_split(const int32_t* __restrict__ seqlen, i
       si.n_split = __builtin_amdgcn_readlane(n, o);
       si.first = base + excl;
       si.chunk = chunk;
+      si.len = __builtin_amdgcn_readlane(len, o);  // the row's length, already in lane o
       return true;
     }
     base += __builtin_amdgcn_readlane(incl, 63);
@@ -237,7 +245,7 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(
   if (!plan_split(seqlen, a.B, capacity, batch, a.target, blockIdx.x, si)) return;  // uniform
   const int b = si.b, split = si.split, n_split_b = si.n_split, first_slot = si.first;
   const int chunk = si.chunk;
-  const int len = clamp_len(seqlen[b], capacity);
+  const int len = si.len;
   const int t_begin = split * chunk;
   const int t_end = min(len, t_begin + chunk);
   if (split == 0 && blockIdx.y == 0 && tid == 0) {
