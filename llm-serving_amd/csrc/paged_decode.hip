@@ -394,6 +394,16 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(
   uint4 kA[U], vA[U], kB[U], vB[U];
   load_pages(t_begin, pgA);
   load_pages(t_begin + batch, pgB);
+  if constexpr (UP) {
+    // all 2U block-table loads go out before the first wait (left alone, the compiler
+    // waits after each scalar load: 2U round trips before the first K/V load, not one)
+    if constexpr (U == 4) {
+      asm volatile("" : "+s"(pgA[0]), "+s"(pgA[1]), "+s"(pgA[2]), "+s"(pgA[3]), "+s"(pgB[0]),
+                        "+s"(pgB[1]), "+s"(pgB[2]), "+s"(pgB[3]));
+    } else if constexpr (U == 2) {
+      asm volatile("" : "+s"(pgA[0]), "+s"(pgA[1]), "+s"(pgB[0]), "+s"(pgB[1]));
+    }
+  }
   issue(t_begin, pgA, kA, vA);
   issue(t_begin + batch, pgB, kB, vB);  // unconditional (see above); n_b >= 1 always
   load_pages(t_begin + 2 * batch, pgA);
@@ -473,60 +483,78 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(
   }
 }
 
+// Eight asm operands x[o] .. x[o + 7] with constraint C.
+#define MI_PIN8(C, x, o)                                                                 \
+  C(x[o]), C(x[o + 1]), C(x[o + 2]), C(x[o + 3]), C(x[o + 4]), C(x[o + 5]), C(x[o + 6]), \
+      C(x[o + 7])
+
 // Second launch, one workgroup per (query head, row), one thread per element of D:
 // zero-length rows get exact zeros; rows split over several workgroups get the
-// log-sum-exp merge of their partials, folded online (running max) 16 splits at a time
-// with every load of a chunk in flight together -- no LDS, no barrier: one round trip for
-// the row's (first slot, split count) record written by the first launch, then one per 16
-// splits. Single-split rows were finished by the first launch.
+// log-sum-exp merge of their partials, folded online (running max) 32 splits at a time --
+// no LDS, no barrier. Three round trips: the arguments, then the row's length with its
+// (first slot, split count) record written by the first launch, then the partials of up to
+// 32 splits at once (lane j of each 32-lane half loads split j's (m, l), every thread the
+// 32 elements of its d); rows of more than 32 splits take one more per 32. Single-split
+// rows were finished by the first launch.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void paged_decode_merge_kernel(
     const int32_t* __restrict__ seqlen, const int32_t* __restrict__ ws_rows,
     const float* __restrict__ ws_ml, const float* __restrict__ ws_acc, T* __restrict__ out,
     DecodeArgs a) {
-  constexpr int kChunk = 16;
+  constexpr int kChunk = 32;  // one split per lane of a 32-lane half; the pin names 32
   const int h = blockIdx.x;
   const int b = blockIdx.y;
-  const int d = threadIdx.x;
+  const int d = threadIdx.x;  // the launch has max(D, 64) threads: whole waves
+  const int lane = d & 63;
   const int capacity = a.max_blocks << a.bs_log2;
-  const int len = clamp_len(seqlen[b], capacity);
-  const int first = ws_rows[2 * b];      // read before the branch: both loads in flight
-  const int n_split = ws_rows[2 * b + 1];
-  if (d >= D) return;
+  // the arguments on other kernarg lines than the row pointers' are loaded with those
+  // (left alone, the compiler loads them after the row's record, each line a scalar-cache
+  // miss of its own)
+  asm volatile("" ::"s"(a.slots), "s"(a.os0), "s"(a.os1), "s"(capacity));
+  // the row's length and its record go out together, one round trip (left alone, the
+  // compiler loads the record only after the length's branch: two more)
+  int len_raw = seqlen[b];
+  int first = ws_rows[2 * b];
+  int n_split = ws_rows[2 * b + 1];
+  asm volatile("" : "+s"(len_raw), "+s"(first), "+s"(n_split));
+  const int len = clamp_len(len_raw, capacity);
   T* orow = out + b * a.os0 + h * a.os1;
   if (len == 0) {
-    orow[d] = from_f32<T>(0.0f);
+    if (d < D) orow[d] = from_f32<T>(0.0f);
     return;
   }
   if (n_split <= 1) return;
+  // threads past D (D < 64) take part in the lane reductions and store nothing
+  const int dl = d < D ? d : D - 1;
   const float* ml = ws_ml + (int64_t(h) * a.slots + first) * 2;  // [head][slot] layout
-  const float* acc = ws_acc + (int64_t(h) * a.slots + first) * D + d;
+  const float* acc = ws_acc + (int64_t(h) * a.slots + first) * D + dl;
   float M = -INFINITY, Ls = 0.0f, As = 0.0f;
   for (int s0 = 0; s0 < n_split; s0 += kChunk) {
-    float m[kChunk], l[kChunk], v[kChunk];
+    const int js = s0 + (lane & (kChunk - 1));
+    // past the row's last split the loads repeat it (valid memory); weighted out below
+    const float2 mlj = *reinterpret_cast<const float2*>(ml + min(js, n_split - 1) * 2);
+    float mx = mlj.x, lx = mlj.y;
+    float v[kChunk];
 #pragma unroll
-    for (int j = 0; j < kChunk; ++j) {
-      const int sp = min(s0 + j, n_split - 1);  // repeated tail entries are weighted out below
-      m[j] = ml[sp * 2];
-      l[j] = ml[sp * 2 + 1];
-      v[j] = acc[int64_t(sp) * D];
-    }
-    float Mc = M;
-#pragma unroll
-    for (int j = 0; j < kChunk; ++j) Mc = s0 + j < n_split ? fmaxf(Mc, m[j]) : Mc;
+    for (int j = 0; j < kChunk; ++j) v[j] = acc[int64_t(min(s0 + j, n_split - 1)) * D];
+    // every load of the chunk is issued before the first wait
+    asm volatile("" : "+v"(mx), "+v"(lx), MI_PIN8("+v", v, 0), MI_PIN8("+v", v, 8),
+                      MI_PIN8("+v", v, 16), MI_PIN8("+v", v, 24));
+    const bool valid = js < n_split;
+    const float Mc = fmaxf(M, group_allreduce<kChunk, MaxOp>(valid ? mx : -INFINITY));
     const float Mu = Mc == -INFINITY ? 0.0f : Mc;
     const float r = fast_exp2(M - Mu);
-    Ls *= r;
+    const float w = valid ? fast_exp2(mx - Mu) : 0.0f;  // split js's weight, in its lane
+    Ls = fmaf(Ls, r, group_allreduce<kChunk, SumOp>(lx * w));
     As *= r;
 #pragma unroll
     for (int j = 0; j < kChunk; ++j) {
-      const float w = s0 + j < n_split ? fast_exp2(m[j] - Mu) : 0.0f;
-      Ls = fmaf(l[j], w, Ls);
-      As = fmaf(v[j], w, As);
+      const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j));
+      As = fmaf(v[j], wj, As);
     }
     M = Mc;
   }
-  orow[d] = from_f32<T>(As / fmaxf(Ls, 1.0f));
+  if (d < D) orow[d] = from_f32<T>(As / fmaxf(Ls, 1.0f));
 }
 
 int ilog2_exact(int x) {
