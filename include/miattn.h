@@ -63,7 +63,7 @@ enum mi_status {
 /* Message of the last failing call on this host thread ("" when none). */
 const char* mi_last_error(void);
 
-/* ABI version: bumps whenever a signature below changes. */
+/* ABI version: bumps whenever a signature below or a layout it documents changes. */
 int mi_abi_version(void);
 
 /* ------------------------------------------------------------------ KV slot write
@@ -258,8 +258,9 @@ int mi_paged_decode_noalloc(const void* q, const void* k_cache, const void* v_ca
  * the staged and ring schedules:
  * {n_work, n_merge, n_partials, layout}, then n_work work entries and n_merge merge
  * entries of two words each; the duo schedule is {n_workgroups, n_merge, n_partials,
- * layout}, n_workgroups {first item word, item count} pairs, the merge entries, then the
- * items of four words each. It returns the word count (host_schedule = NULL sizes it).
+ * layout}, n_workgroups entries of eight words {first item word, item count, the first
+ * item's four words, 0, 0}, the merge entries of two words each, then the items of four
+ * words each. It returns the word count (host_schedule = NULL sizes it).
  * It depends only on the segment lengths, H and head_dim, so a caller builds it once per
  * packed group and reuses it for every layer, passing the four header words to
  * mi_varlen_prefill.

@@ -989,6 +989,9 @@ struct Duo {
   // so their lane offsets differ by a constant
   static constexpr int LOAD_PERIOD = (WAVES * RPS) % SW_PERIOD == 0 ? 1 : SW_PERIOD / (WAVES * RPS);
   static constexpr int ITEM_WORDS = 4;        // {seq0, L, tile << 16 | split << 8 | n_split - 1, h << 24 | slot}
+  // a workgroup's table entry: {first item word, item count, its first item's words, 0, 0},
+  // so that a fresh workgroup reads its first item in the same round trip as its entry
+  static constexpr int ENTRY_WORDS = 8;
   static_assert(D == 64 || D == 128 || D == 256, "duo kernel head dims");
   static_assert(SEGS % WAVES == 0 && LPW % LOAD_PERIOD == 0 && (WAVES * RPS * LOAD_PERIOD) % SW_PERIOD == 0,
                 "whole loads per wave, swizzle periodic in the loads");
@@ -1017,9 +1020,21 @@ __global__ __launch_bounds__(Duo<D>::THREADS, Duo<D>::PER_CU) void varlen_prefil
   __shared__ __align__(512) uint8_t vb1[W::BUFB];
   __shared__ float mlx[2][2][2][64];  // [key half][query block][m, l][lane]
 
-  // this workgroup's item list: {first word, count}
-  const int first = sched[kSchedHeader + 2 * blockIdx.x];
-  const int count = sched[kSchedHeader + 2 * blockIdx.x + 1];
+  // every argument is loaded with the schedule pointer (left alone, the compiler loads the
+  // rest after the table entry: one or two more round trips before the first DMA); at
+  // head_dim 256 the tensor pointers stay lazily loaded (held from the start they push the
+  // lone wave's 512 registers into spills)
+  if constexpr (D != 256) asm volatile("" ::"s"(q), "s"(k), "s"(v), "s"(out), "s"(partials));
+  asm volatile("" ::"s"(H), "s"(H_kv), "s"(G), "s"(scale_log2), "s"(causal));
+  // this workgroup's table entry: {first word of its item list, count, item 0's words}, all
+  // loaded before the first wait (left alone, the compiler waits for the count's branch)
+  const int32_t* entry = sched + kSchedHeader + W::ENTRY_WORDS * blockIdx.x;
+  int first = entry[0], count = entry[1];
+  int iw[W::ITEM_WORDS];
+#pragma unroll
+  for (int j = 0; j < W::ITEM_WORDS; ++j) iw[j] = entry[2 + j];
+  static_assert(W::ITEM_WORDS == 4, "the pin below names four item words");
+  asm volatile("" : "+s"(first), "+s"(count), "+s"(iw[0]), "+s"(iw[1]), "+s"(iw[2]), "+s"(iw[3]));
   if (count <= 0) return;
 
   const int tid = threadIdx.x;
@@ -1036,7 +1051,7 @@ __global__ __launch_bounds__(Duo<D>::THREADS, Duo<D>::PER_CU) void varlen_prefil
     int seq0, L, row0, split, n_split, slot, h, t_first, t_end;
   };
   // an item's words are loaded (scalar) while the previous item runs, decoded when needed
-  int iw[W::ITEM_WORDS];
+  // (item 0's came with the table entry)
   auto load_words = [&](int i) {
     const int32_t* w = sched + first + W::ITEM_WORDS * i;
 #pragma unroll
@@ -1161,7 +1176,6 @@ __global__ __launch_bounds__(Duo<D>::THREADS, Duo<D>::PER_CU) void varlen_prefil
 
   // first item: Q, K(t0), K(t0+1) and V(t0) in flight (later items get them from the
   // previous item's epilogue)
-  load_words(0);
   Item it = decode();
   const char* kseg = seg_of(k, it);
   const char* vseg = seg_of(v, it);
@@ -1599,15 +1613,16 @@ int launch2(const void* q, const void* k, const void* v, void* out, const int32_
           }
         }
       } else if (kind == kDuo) {
-        // n_work persistent workgroups; their item table follows the header, the merge
-        // entries follow the table
+        // n_work persistent workgroups; their table follows the header, the merge entries
+        // follow the table
         hipLaunchKernelGGL((varlen_prefill_duo_kernel<T, D>), dim3(n_work), dim3(Duo<D>::THREADS), 0, s,
                            static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
                            static_cast<T*>(out), sched, partials, H, H_kv, H / H_kv, scale_log2, causal);
         if (n_merge > 0) {
           hipLaunchKernelGGL((varlen_prefill_merge_kernel<T, D, Duo<D>::BQ>),
                              dim3(H, n_merge, (Duo<D>::BQ + kRowsPerBlock - 1) / kRowsPerBlock), dim3(256), 0, s,
-                             cu, work + 2 * n_work, static_cast<const float*>(partials), static_cast<T*>(out), H);
+                             cu, work + Duo<D>::ENTRY_WORDS * n_work, static_cast<const float*>(partials),
+                             static_cast<T*>(out), H);
         }
       }
       return launch_status("mi_varlen_prefill");
@@ -1638,9 +1653,9 @@ int launch1(int D, const void* q, const void* k, const void* v, void* out, const
 // (n_split - 1) << 24 | first partial slot), or a merge entry, with its cost in key tiles.
 struct Piece { int work, w0, w1; };
 
-// Persistent duo kernel schedule: {n_wg, n_merge, n_partials, layout}, then n_wg entries
-// {first item word, item count}, the n_merge merge entries, and the items, Duo::ITEM_WORDS
-// words each. Items are (piece, head) pairs dealt out longest-first to the workgroup with
+// Persistent duo kernel schedule: {n_wg, n_merge, n_partials, layout}, then n_wg entries of
+// Duo::ENTRY_WORDS {first item word, item count, the first item's words, 0, 0}, the n_merge
+// merge entries, and the items, Duo::ITEM_WORDS words each. Items are (piece, head) pairs dealt out longest-first to the workgroup with
 // the least work so far (LPT); when the KV heads divide evenly over the XCDs, the items of
 // a KV head go to the workgroups of one XCD (workgroup w runs on XCD w % kXcds), so its K
 // and V stay in that XCD's L2. An item costs its key tiles plus kItemOverhead for its
@@ -1654,7 +1669,8 @@ int duo_schedule(const int32_t* cu, const std::vector<Piece>& pieces, const std:
   const int64_t n_items = int64_t(pieces.size()) * H;
   const int n_wg = int(std::min<int64_t>(kSlots, n_items));
   const int n_merge = int(merges.size());
-  const int64_t words64 = kSchedHeader + 2 * int64_t(n_wg) + 2 * int64_t(n_merge) + Duo<128>::ITEM_WORDS * n_items;
+  constexpr int EW = Duo<128>::ENTRY_WORDS, IW = Duo<128>::ITEM_WORDS;
+  const int64_t words64 = kSchedHeader + EW * int64_t(n_wg) + 2 * int64_t(n_merge) + IW * n_items;
   if (words64 > INT32_MAX) return fail(MI_ERR_UNSUPPORTED, "mi_varlen_schedule: schedule too large");
   const int words = int(words64);
   if (out == nullptr) return words;
@@ -1687,23 +1703,28 @@ int duo_schedule(const int32_t* cu, const std::vector<Piece>& pieces, const std:
   out[2] = n_partials;
   out[3] = layout_word(kDuo, D, Duo<128>::BQ);
   int32_t* table = out + kSchedHeader;
-  int32_t* mw = table + 2 * n_wg;
+  int32_t* mw = table + EW * n_wg;
   for (const Piece& pc : merges) { *mw++ = pc.w0; *mw++ = pc.w1; }
   int item_word = int(mw - out);
   int32_t* iw = mw;
   for (int w = 0; w < n_wg; ++w) {
-    table[2 * w] = item_word;
-    table[2 * w + 1] = int(lists[w].size());
-    for (int id : lists[w]) {
+    int32_t* e = table + EW * w;
+    std::fill(e, e + EW, 0);
+    e[0] = item_word;
+    e[1] = int(lists[w].size());
+    for (size_t i = 0; i < lists[w].size(); ++i) {
+      const int id = lists[w][i];
       const Piece& pc = pieces[id / H];
       const int h = id % H;
       const int seq = int(uint32_t(pc.w0) >> 16), tile = pc.w0 & 0xffff;
       const int split = int(uint32_t(pc.w1) >> 28), nsm1 = (pc.w1 >> 24) & 15, slot = pc.w1 & 0xffffff;
-      *iw++ = cu[seq];
-      *iw++ = cu[seq + 1] - cu[seq];
-      *iw++ = int((uint32_t(tile) << 16) | (uint32_t(split) << 8) | uint32_t(nsm1));
-      *iw++ = int((uint32_t(h) << 24) | uint32_t(slot));
-      item_word += Duo<128>::ITEM_WORDS;
+      iw[0] = cu[seq];
+      iw[1] = cu[seq + 1] - cu[seq];
+      iw[2] = int((uint32_t(tile) << 16) | (uint32_t(split) << 8) | uint32_t(nsm1));
+      iw[3] = int((uint32_t(h) << 24) | uint32_t(slot));
+      if (i == 0) std::copy(iw, iw + IW, e + 2);  // the first item, inline
+      iw += IW;
+      item_word += IW;
     }
   }
   return words;

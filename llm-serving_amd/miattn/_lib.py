@@ -126,7 +126,7 @@ SIGNATURES: dict[str, tuple] = {
     ),
 }
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 
 def _load():

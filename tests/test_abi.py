@@ -91,22 +91,25 @@ def _schedule(lengths, H=16, H_kv=8, D=128, causal=1, kernel=None):
 
 def _duo_schedule(out, words, lengths, cu, H, H_kv, D):
     """Parse and check the persistent duo kernel's schedule: {n_wg, n_merge, n_partials,
-    layout}, n_wg {first item word, count} entries, the merges, then 4-word items {seq0, L,
-    tile << 16 | split << 8 | n_split - 1, head << 24 | slot}. Returns the pieces of head 0
-    in the common (seq, tile, split, n_split, slot) form, after checking every head has the
-    same pieces."""
+    layout}, n_wg 8-word entries {first item word, count, the first item's 4 words, 0, 0},
+    the merges, then 4-word items {seq0, L, tile << 16 | split << 8 | n_split - 1,
+    head << 24 | slot}. Returns the pieces of head 0 in the common (seq, tile, split,
+    n_split, slot) form, after checking every head has the same pieces."""
     n_wg, n_merge, n_partials, layout = out[0], out[1], out[2], out[3]
     assert layout == (3 << 20) | (D << 8) | 64 and 1 <= n_wg <= 512
     u = [out[i] & 0xFFFFFFFF for i in range(words)]
-    merges = [(u[4 + 2 * n_wg + 2 * i] >> 16, u[4 + 2 * n_wg + 2 * i] & 0xFFFF, u[5 + 2 * n_wg + 2 * i] >> 24,
-               u[5 + 2 * n_wg + 2 * i] & 0xFFFFFF) for i in range(n_merge)]
-    item_base = 4 + 2 * n_wg + 2 * n_merge
+    mb = 4 + 8 * n_wg
+    merges = [(u[mb + 2 * i] >> 16, u[mb + 2 * i] & 0xFFFF, u[mb + 1 + 2 * i] >> 24, u[mb + 1 + 2 * i] & 0xFFFFFF)
+              for i in range(n_merge)]
+    item_base = mb + 2 * n_merge
     seq_of = {c: i for i, c in enumerate(cu[:-1])}
     per_head = {h: [] for h in range(H)}
     seen_words = 0
     for wg in range(n_wg):
-        first, count = out[4 + 2 * wg], out[5 + 2 * wg]
+        entry = out[4 + 8 * wg: 12 + 8 * wg]
+        first, count = entry[0], entry[1]
         assert first == item_base + seen_words and count >= 1
+        assert list(entry[2:6]) == list(out[first:first + 4]) and list(entry[6:]) == [0, 0]  # item 0 inline
         costs = []
         for i in range(count):
             seq0, L, w2, w3 = (u[first + 4 * i + j] for j in range(4))
