@@ -340,3 +340,23 @@ def test_zero_length_rows_next_to_long_rows(cuda):
             assert not got[r].any()
     expected = reference_paged_decode(*_cpu(q, k, v, table, seqlen), out_dtype=torch.float32)
     assert (got.float() - expected).abs().max().item() <= 2e-2
+
+
+@pytest.mark.parametrize("H,H_kv,D,length", [
+    (16, 8, 128, 9), (16, 8, 128, 248), (16, 8, 128, 256), (16, 8, 128, 257), (16, 8, 128, 512),
+    (16, 8, 128, 520), (16, 8, 128, 4096), (8, 2, 256, 264),
+])
+def test_merge_chunk_boundaries(H, H_kv, D, length, cuda):
+    """The merge launch folds a row's split partials 32 at a time (one split per lane of a
+    32-lane half, then a lane reduction). One row at these shapes is planned in 8-token
+    splits (512 split target, one workgroup column), so a row of L tokens has ceil(L / 8)
+    partials: 2, 31, 32, 33 (a full chunk and one more), 64, 65 and 512 (16 chunks), and
+    33 at the Qwen3.5 shape; each is checked against the fp32 gather oracle and the
+    north-star bar."""
+    q, k, v, table, seqlen = _build(1, H, H_kv, D, 16, [length], dtype=torch.bfloat16, seed=length)
+    got = paged_decode(q, k, v, table, seqlen)
+    torch.cuda.synchronize()
+    expected = reference_paged_decode(*_cpu(q, k, v, table, seqlen), out_dtype=torch.float32)
+    diff = (got.cpu().float() - expected).abs()
+    assert diff.max().item() < 2e-2
+    assert (diff - expected.abs() * 2.0 ** -8).max().item() <= 1e-3
