@@ -440,6 +440,22 @@ def bench_block32(stream, steps: int = 50) -> dict:
             "frac_hbm_peak": res["gbs"] / HBM_PEAK_GBS}
 
 
+def bench_head_major(stream, steps: int = 50) -> dict:
+    """Config 2 with head-major pools: each layer's K and V stored as (n_blocks, H_kv, 16,
+    128), so a block holds each KV head's 16 tokens contiguously, and passed as the
+    (n_blocks, 16, H_kv, 128) view with those strides; the same lengths, tables and bytes,
+    checked then timed like the headline leg."""
+    from miattn import workloads as W
+
+    inp = W.paged_decode_config(device="cuda", head_major=True)
+    res = bench_decode(inp, steps, 5, stream)
+    res.pop("out0")
+    del inp
+    torch.cuda.empty_cache()
+    return {"workload": "config2 lengths, head-major pools (n_blocks, H_kv, 16, D), 28 layers, HIP-graph replay",
+            **res, "frac_hbm_peak": res["gbs"] / HBM_PEAK_GBS}
+
+
 def check_decode_rows(inp, out0, rows) -> float:
     """Layer 0's output rows ``rows`` against the fp32 gather oracle (oracle.decode), before
     anything is timed; returns max|delta| and exits when it is outside the bf16 bar."""
@@ -689,6 +705,8 @@ def main() -> int:
         log("block size 32 (config 2 lengths)")
         line["decode_block32"] = bench_block32(stream)
         log(f"bs32: {line['decode_block32']['us_per_layer']:.2f} us/layer")
+        line["decode_head_major"] = bench_head_major(stream)
+        log(f"head-major pools: {line['decode_head_major']['us_per_layer']:.2f} us/layer")
         log("long-context decode (config 4)")
         line["long_context"] = bench_long_context(stream)
         log(f"config4: {line['long_context']['gbs']:.1f} GB/s")

@@ -122,10 +122,14 @@ def paged_decode_config(
     *, B: int = 32, lengths=None, lo: int = 128, hi: int = 2048, n_blocks: int = 8192,
     n_layer: int = 28, seed: int = 2, device="cuda", dtype=torch.bfloat16, max_blocks: int | None = None,
     H: int | None = None, H_kv: int | None = None, D: int | None = None, block_size: int | None = None,
+    head_major: bool = False,
 ) -> PagedDecodeInputs:
     """Configs 2 and 4: a paged pool per layer, disjoint permuted tables, seqlen per row.
 
     ``lengths`` overrides the U[lo, hi] draw (config 4 passes ``[8192] * 32``).
+    ``head_major`` stores each pool as (n_blocks, H_kv, block_size, D) in memory (each KV
+    head's tokens of a block contiguous) and hands out its (n_blocks, block_size, H_kv, D)
+    view, the reference's logical layout, with the strides of the head-major storage.
     """
     H = H or QWEN3_ATTN["H"]
     H_kv = H_kv or QWEN3_ATTN["H_kv"]
@@ -142,9 +146,14 @@ def paged_decode_config(
         table[row, : len(t)] = torch.tensor(t, dtype=torch.int32)
     dev = torch.device(device)
     dgen = torch.Generator(device=dev).manual_seed(seed + 2)
-    shape = (n_blocks, bs, H_kv, D)
-    k_caches = [_randn(shape, dgen, dev, dtype) for _ in range(n_layer)]
-    v_caches = [_randn(shape, dgen, dev, dtype) for _ in range(n_layer)]
+    if head_major:
+        shape = (n_blocks, H_kv, bs, D)
+        k_caches = [_randn(shape, dgen, dev, dtype).permute(0, 2, 1, 3) for _ in range(n_layer)]
+        v_caches = [_randn(shape, dgen, dev, dtype).permute(0, 2, 1, 3) for _ in range(n_layer)]
+    else:
+        shape = (n_blocks, bs, H_kv, D)
+        k_caches = [_randn(shape, dgen, dev, dtype) for _ in range(n_layer)]
+        v_caches = [_randn(shape, dgen, dev, dtype) for _ in range(n_layer)]
     q = [_randn((B, H, D), dgen, dev, dtype) for _ in range(n_layer)]
     return PagedDecodeInputs(q, k_caches, v_caches, table.to(dev), torch.tensor(lengths, dtype=torch.int32, device=dev),
                              tables, lengths, bs)

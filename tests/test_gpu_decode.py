@@ -360,3 +360,27 @@ def test_merge_chunk_boundaries(H, H_kv, D, length, cuda):
     diff = (got.cpu().float() - expected).abs()
     assert diff.max().item() < 2e-2
     assert (diff - expected.abs() * 2.0 ** -8).max().item() <= 1e-3
+
+
+@pytest.mark.parametrize("H,H_kv,D,bs,lengths", [
+    (16, 8, 128, 16, [2048, 700, 129, 5, 0, 1]),
+    (8, 2, 256, 32, [1664, 33, 4097]),
+], ids=["qwen3", "qwen35-bs32"])
+def test_head_major_pools(H, H_kv, D, bs, lengths, cuda):
+    """Pools stored head-major, (n_blocks, H_kv, block_size, D) in memory, passed as the
+    reference's (n_blocks, block_size, H_kv, D) view with those strides (the layout
+    question of the next-rows list): same output as the token-major pools, through
+    paged_decode and through a plan."""
+    B = len(lengths)
+    q, k, v, table, seqlen = _build(B, H, H_kv, D, bs, lengths, dtype=torch.bfloat16, seed=77)
+    k_hm = k.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)
+    v_hm = v.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)
+    assert torch.equal(k_hm, k) and k_hm.stride() != k.stride()
+    ref = paged_decode(q, k, v, table, seqlen)
+    got = paged_decode(q, k_hm, v_hm, table, seqlen)
+    plan = paged_decode_plan(q, [k_hm], [v_hm], table, seqlen)
+    got_plan = plan.run(0, q)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref) and torch.equal(got_plan, ref)
+    expected = reference_paged_decode(*_cpu(q, k, v, table, seqlen), out_dtype=torch.float32)
+    assert (got.cpu().float() - expected).abs().max().item() < 2e-2
