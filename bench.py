@@ -223,7 +223,9 @@ def bench_prefill(stream, steps: int = 20, eager: bool = False):
                 write_step()
             write_step_ms = t.ms()
     else:
-        write_step_ms, _ = time_graph(write_step, stream, steps, 3)
+        # a write step is ~0.25 ms: at least 100 replays, so the figure is not a few ms of
+        # samples
+        write_step_ms, _ = time_graph(write_step, stream, max(steps, 100), 3)
     pool.check_writes()
     write_ms = write_step_ms / N_LAYER
     write_bytes = 2 * 2 * sum(inp.lengths) * inp.k.shape[1] * D * 2 + sum(inp.lengths) * 8
