@@ -556,6 +556,7 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(
   }
   if (d < D) orow[d] = from_f32<T>(As / fmaxf(Ls, 1.0f));
 }
+#undef MI_PIN8
 
 int ilog2_exact(int x) {
   int lg = 0;
