@@ -531,7 +531,8 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
 // at each barrier of the ring and duo kernels: (1) a tile read after it was waited for, by
 // every wave, for that wave's own loads of it (vmcnt(N), N = loads issued after them; they
 // retire in order); (2) a buffer refilled after it is no longer read by any wave before
-// it (lgkmcnt(0) in the same wait).
+// it (lgkmcnt(0) in the same wait). The duo kernel's head_dim 256 steps keep both rules
+// over pairs of waves instead (pair_sync in that kernel).
 __device__ __forceinline__ void bare_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 template <typename T, int D>
@@ -1081,24 +1082,57 @@ __global__ __launch_bounds__(Duo<D>::THREADS, Duo<D>::PER_CU) void varlen_prefil
   // item's KV head, range = the tile's rows inside the segment (rows past it read as zero; a
   // tile past the item reads nothing), so a step builds two resources and no per-load scalar
   // arithmetic.
-  constexpr int LP = W::LOAD_PERIOD;
+  //
+  // At head_dim 256 (one workgroup per CU, one wave per SIMD) the K/V tiles are loaded
+  // pair-locally instead: the rows of key half kh come only from the two waves that read
+  // them, (0, kh) and (1, kh), wave (qb, kh) taking segments kh * SEGS/2 + qb + 2i, so a
+  // step ends with a sync of those two waves (pair_sync below) instead of the workgroup
+  // barrier that lock-steps all four (its sw(row) repeats every SW_PERIOD / (2 RPS) loads).
+  constexpr bool kPairSync = D == 256;
+  constexpr int LP = kPairSync ? W::SW_PERIOD / (2 * W::RPS) : W::LOAD_PERIOD;
+  static_assert(!kPairSync || (LPW % LP == 0 && (W::SEGS / 2 * W::RPS) % W::SW_PERIOD == 0 &&
+                               2 * LPW == W::SEGS / 2),
+                "pair-local loads: whole swizzle periods, each pair covering its key half");
+  auto seg_index = [&](int i) { return kPairSync ? kh * (W::SEGS / 2) + qb + 2 * i : wave + i * W::WAVES; };
   int dma_off[LP];
 #pragma unroll
   for (int p = 0; p < LP; ++p) {
-    const int r = (wave + p * W::WAVES) * W::RPS + lane / W::NCH;
+    const int r = seg_index(p) * W::RPS + lane / W::NCH;
     dma_off[p] = int(r * kv_row_b) + (((lane % W::NCH) ^ W::sw(r)) << 4);
   }
-  const int dma_step = int(W::WAVES * W::RPS * LP * kv_row_b);
+  const int dma_step = int((seg_index(LP) - seg_index(0)) * W::RPS * kv_row_b);
   auto issue = [&](const char* seg, const Item& it, int t, uint8_t* dst) {
     const int rows = t < it.t_end ? min(it.L - t * BK, BK) : 0;
     const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(seg + int64_t(t) * (BK * kv_row_b)), (short)0,
                                                       rows * int(kv_row_b), 0x00020000);
 #pragma unroll
     for (int i = 0; i < LPW; ++i) {
-      buffer_load_lds16(rs, (lds_void_t*)((__attribute__((address_space(3))) uint8_t*)dst + (wave + i * W::WAVES) * 1024),
+      buffer_load_lds16(rs, (lds_void_t*)((__attribute__((address_space(3))) uint8_t*)dst + seg_index(i) * 1024),
                         dma_off[i % LP] + (i / LP) * dma_step);
     }
   };
+  // Pair sync (head_dim 256): after its own loads of the step's tiles have landed and its
+  // reads of them are done (the caller's wait), a wave publishes its step count in LDS and
+  // waits until its partner's has caught up. Both waves of a pair run the same steps, so
+  // the counts meet; the wait gives up after kPairSpinMax polls (a broken count then shows
+  // as wrong output in the tests, never as a hang).
+  constexpr int kPairSpinMax = 1 << 20;
+  __shared__ int pflag[W::WAVES];
+  int gstep = 0;
+  auto pair_sync = [&]() {
+    ++gstep;
+    asm volatile("" ::: "memory");
+    __hip_atomic_store(&pflag[wave], gstep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    for (int spin = 0; spin < kPairSpinMax; ++spin) {
+      const int seen = __builtin_amdgcn_readfirstlane(
+          __hip_atomic_load(&pflag[wave ^ 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+      if (seen >= gstep) break;  // (polled without s_sleep: 43.7 against 46.3 us with it)
+    }
+    asm volatile("" ::: "memory");
+  };
+  if constexpr (kPairSync) {
+    if (tid < W::WAVES) pflag[tid] = 0;  // read after the first item's barrier
+  }
   // the item's K and V at its segment's first token and its KV head
   auto seg_of = [&](const T* base, const Item& it) {
     return reinterpret_cast<const char*>(base) + int64_t(it.seq0) * kv_row_b + (it.h / G) * ROWB;
@@ -1353,7 +1387,11 @@ __global__ __launch_bounds__(Duo<D>::THREADS, Duo<D>::PER_CU) void varlen_prefil
       cur = nxt;
       __builtin_amdgcn_s_setprio(0);
       wait_vm_lgkm0<0>();
-      bare_barrier();
+      if constexpr (kPairSync) {
+        pair_sync();
+      } else {
+        bare_barrier();
+      }
     };
     using NoPV = std::false_type;
     using PV = std::true_type;
