@@ -1372,8 +1372,9 @@ __global__ __launch_bounds__(Duo<D>::THREADS, Duo<D>::PER_CU) void varlen_prefil
           __builtin_amdgcn_sched_group_barrier(0x0002, kPV ? 5 : 9, 0);
         }
       } else {
-        // the second half's reads go out behind the first half's MFMAs
-        __builtin_amdgcn_sched_barrier(0);
+        // the second half scheduled freely against the first half's MFMAs: behind a
+        // sched_barrier the compiler read its fragments one at a time, each waited for
+        // before its MFMA (43.9 against 43.4 us at head_dim 256)
         read_part(1);
         mfma_part(1);
       }
