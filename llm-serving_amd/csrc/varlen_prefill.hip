@@ -1313,7 +1313,16 @@ __global__ __launch_bounds__(Duo<D>::THREADS, Duo<D>::PER_CU) void varlen_prefil
       // workgroup-uniform: only a tile that reaches past the segment end or the diagonal
       // needs the mask
       if ((t + 1) * BK > L || (causal && (t + 1) * BK - 1 > it.row0)) {
-        const int lim = (causal ? min(L, qi + 1) : L) - (t * BK + kh * 32) - g * 4;  // key offsets < lim are valid
+        // at head_dim 256 the lane's query row and key group are rebuilt here from the lane
+        // id: held through the item loop they were spilled, and the scratch reload's wait
+        // (loads retire in order) also waited for the step's K/V loads just issued
+        int lim;  // key offsets < lim are valid
+        if constexpr (D == 256) {
+          const int ml = __lane_id();
+          lim = (causal ? min(L, it.row0 + qb * 32 + (ml & 31) + 1) : L) - (t * BK + kh * 32) - (ml >> 5) * 4;
+        } else {
+          lim = (causal ? min(L, qi + 1) : L) - (t * BK + kh * 32) - g * 4;
+        }
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           if ((e >> 2) * 8 + (e & 3) >= lim) sc[e] = -INFINITY;
