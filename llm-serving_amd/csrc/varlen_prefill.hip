@@ -1703,10 +1703,11 @@ struct Piece { int work, w0, w1; };
 
 // Persistent duo kernel schedule: {n_wg, n_merge, n_partials, layout}, then n_wg entries of
 // Duo::ENTRY_WORDS {first item word, item count, the first item's words, 0, 0}, the n_merge
-// merge entries, and the items, Duo::ITEM_WORDS words each. Items are (piece, head) pairs dealt out longest-first to the workgroup with
-// the least work so far (LPT); when the KV heads divide evenly over the XCDs, the items of
-// a KV head go to the workgroups of one XCD (workgroup w runs on XCD w % kXcds), so its K
-// and V stay in that XCD's L2. An item costs its key tiles plus kItemOverhead for its
+// merge entries, and the items, Duo::ITEM_WORDS words each. Items are (piece, head) pairs
+// dealt out longest-first to the workgroup with the least work so far (LPT); when the launch
+// fills the chip and the KV heads divide evenly over the XCDs, or the XCDs over the KV heads,
+// the items of a KV head go to the workgroups of its XCD or block of XCDs (workgroup w runs on
+// XCD w % kXcds), so its K and V stay in those XCDs' L2. An item costs its key tiles plus kItemOverhead for its
 // prologue and epilogue: a workgroup's extra single-tile item takes about as long as five
 // 64-key steps, and counting 8 balances best (config-3 batch 31.5 us against 32.2 us with
 // 3, 31.8 with 12, 32.9 with 16; batches of equal or mid-length segments unchanged).
@@ -1724,20 +1725,28 @@ int duo_schedule(const int32_t* cu, const std::vector<Piece>& pieces, const std:
   if (out == nullptr) return words;
   if (capacity < words) return fail(MI_ERR_INVALID, "mi_varlen_schedule: capacity %d < %d words", capacity, words);
   // groups of workgroups that share an L2: one per XCD when the KV heads spread evenly
-  const bool affine = n_wg == kSlots && H_kv % kXcds == 0;
-  const int n_groups = affine ? kXcds : 1;
+  // KV heads per XCD group: with H_kv a multiple of the XCD count each XCD takes the KV
+  // heads kvh with kvh % kXcds == x; with H_kv a divisor of it each KV head takes a block of
+  // kXcds / H_kv XCDs (at H_kv 2, XCDs 0-3 and 4-7), so an XCD's L2 holds one KV head's K/V
+  const bool full = n_wg == kSlots;
+  const int n_groups = !full ? 1 : H_kv % kXcds == 0 ? kXcds : kXcds % H_kv == 0 ? H_kv : 1;
+  const int xcds_per_group = kXcds / n_groups;
+  auto group_of_wg = [&](int w) { return (w % kXcds) / xcds_per_group; };
   const int G = H / H_kv;
+  auto group_of_head = [&](int h) { return (h / G) % n_groups; };
   std::vector<std::vector<int>> lists(n_wg);
   std::vector<int64_t> load(n_wg, 0);
   for (int grp = 0; grp < n_groups; ++grp) {
     // workgroups of this group, as a min-heap on (load, id)
     std::vector<std::pair<int64_t, int>> heap;
-    for (int w = grp; w < n_wg; w += n_groups) heap.push_back({0, w});
+    for (int w = 0; w < n_wg; ++w) {
+      if (group_of_wg(w) == grp) heap.push_back({0, w});
+    }
     auto cmp = [](const std::pair<int64_t, int>& a, const std::pair<int64_t, int>& b) { return a > b; };
     std::make_heap(heap.begin(), heap.end(), cmp);
     for (int p = 0; p < int(pieces.size()); ++p) {  // pieces are sorted longest-first
       for (int h = 0; h < H; ++h) {
-        if (affine && (h / G) % kXcds != grp) continue;
+        if (group_of_head(h) != grp) continue;
         std::pop_heap(heap.begin(), heap.end(), cmp);
         auto& top = heap.back();
         lists[top.second].push_back(p * H + h);

@@ -117,8 +117,10 @@ def _duo_schedule(out, words, lengths, cu, H, H_kv, D):
             assert lengths[seq] == L
             tile, split, ns, h, slot = w2 >> 16, (w2 >> 8) & 0xFF, (w2 & 0xFF) + 1, w3 >> 24, w3 & 0xFFFFFF
             per_head[h].append((seq, tile, split, ns, slot))
-            if n_wg == 512 and H_kv % 8 == 0:  # a KV head's items stay on one XCD
+            if n_wg == 256 * (1 if D == 256 else 2) and H_kv % 8 == 0:  # a KV head's items stay on one XCD
                 assert (h // (H // H_kv)) % 8 == wg % 8
+            elif n_wg == 256 * (1 if D == 256 else 2) and 8 % H_kv == 0:  # ... on its block of 8 / H_kv XCDs
+                assert h // (H // H_kv) == (wg % 8) // (8 // H_kv)
             costs.append(_piece_work(lengths, (seq, tile, split, ns, slot), 3))
         assert costs == sorted(costs, reverse=True)  # longest first within a workgroup
         seen_words += 4 * count
@@ -211,6 +213,18 @@ def test_schedule_head_dim_256_runs_the_duo_kernel_one_workgroup_per_cu():
     out = (ctypes.c_int32 * words)()
     assert _lib.lib.mi_varlen_schedule_for(host_cu, 2, 16, 8, 256, 1, -1, out, words) == words
     assert out[0] == 256 and out[3] == (3 << 20) | (256 << 8) | 64  # workgroups, duo layout
+    assert sorted((s, t) for s, t, *_ in pieces) == sorted(
+        {(s, t) for s, n in enumerate(lengths) for t in range(-(-n // 64))})
+
+
+@pytest.mark.parametrize("H,H_kv,D", [(8, 2, 256), (16, 4, 128), (16, 1, 128)])
+def test_schedule_gives_each_kv_head_its_block_of_xcds(H, H_kv, D):
+    """A chip-filling duo launch whose KV heads divide the 8 XCDs deals each KV head's items
+    to the workgroups of its block of 8 / H_kv XCDs (workgroup w on XCD w % 8; checked per
+    item by the parser) and still covers every tile once per head; with one KV head every
+    workgroup takes part."""
+    lengths = [1742, 110, 658, 364, 390, 450, 152, 445]  # config 3
+    (n_work, _, _), pieces, _ = _schedule(lengths, H=H, H_kv=H_kv, D=D)
     assert sorted((s, t) for s, t, *_ in pieces) == sorted(
         {(s, t) for s, n in enumerate(lengths) for t in range(-(-n // 64))})
 
