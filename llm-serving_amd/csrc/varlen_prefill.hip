@@ -532,7 +532,7 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
 // every wave, for that wave's own loads of it (vmcnt(N), N = loads issued after them; they
 // retire in order); (2) a buffer refilled after it is no longer read by any wave before
 // it (lgkmcnt(0) in the same wait). The duo kernel's head_dim 256 steps keep both rules
-// over pairs of waves instead (pair_sync in that kernel).
+// over pairs of waves instead (pair_publish / pair_wait in that kernel).
 __device__ __forceinline__ void bare_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 template <typename T, int D>
@@ -1086,7 +1086,7 @@ __global__ __launch_bounds__(Duo<D>::THREADS, Duo<D>::PER_CU) void varlen_prefil
   // At head_dim 256 (one workgroup per CU, one wave per SIMD) the K/V tiles are loaded
   // pair-locally instead: the rows of key half kh come only from the two waves that read
   // them, (0, kh) and (1, kh), wave (qb, kh) taking segments kh * SEGS/2 + qb + 2i, so a
-  // step ends with a sync of those two waves (pair_sync below) instead of the workgroup
+  // step ends with a sync of those two waves (pair_publish, pair_wait) instead of the workgroup
   // barrier that lock-steps all four (its sw(row) repeats every SW_PERIOD / (2 RPS) loads).
   constexpr bool kPairSync = D == 256;
   constexpr int LP = kPairSync ? W::SW_PERIOD / (2 * W::RPS) : W::LOAD_PERIOD;
@@ -1111,18 +1111,23 @@ __global__ __launch_bounds__(Duo<D>::THREADS, Duo<D>::PER_CU) void varlen_prefil
                         dma_off[i % LP] + (i / LP) * dma_step);
     }
   };
-  // Pair sync (head_dim 256): after its own loads of the step's tiles have landed and its
-  // reads of them are done (the caller's wait), a wave publishes its step count in LDS and
-  // waits until its partner's has caught up. Both waves of a pair run the same steps, so
-  // the counts meet; the wait gives up after kPairSpinMax polls (a broken count then shows
-  // as wrong output in the tests, never as a hang).
+  // Pair sync (head_dim 256): once its own loads of the step's tiles have landed and its
+  // reads of the shared rows are done (the caller's wait, before the step's last MFMAs), a
+  // wave publishes its step count in LDS (pair_publish); at the end of the step it waits
+  // until its partner's count has caught up (pair_wait). Both waves of a pair run the same
+  // steps, so the counts meet; the wait gives up after kPairSpinMax polls (a broken count
+  // then shows as wrong output in the tests, never as a hang).
   constexpr int kPairSpinMax = 1 << 20;
   __shared__ int pflag[W::WAVES];
   int gstep = 0;
-  auto pair_sync = [&]() {
+  auto pair_publish = [&]() {
     ++gstep;
     asm volatile("" ::: "memory");
     __hip_atomic_store(&pflag[wave], gstep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    asm volatile("" ::: "memory");
+  };
+  auto pair_wait = [&]() {
+    asm volatile("" ::: "memory");
     for (int spin = 0; spin < kPairSpinMax; ++spin) {
       const int seen = __builtin_amdgcn_readfirstlane(
           __hip_atomic_load(&pflag[wave ^ 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
@@ -1385,6 +1390,13 @@ __global__ __launch_bounds__(Duo<D>::THREADS, Duo<D>::PER_CU) void varlen_prefil
         // sched_barrier the compiler read its fragments one at a time, each waited for
         // before its MFMA (43.9 against 43.4 us at head_dim 256)
         read_part(1);
+        if constexpr (kPairSync) {
+          // this wave's loads of the step have landed and its reads of the shared rows are
+          // done: published before the half's MFMAs, so the partner waits less (41.8 against
+          // 42.2 us published at the end of the step)
+          wait_vm_lgkm0<0>();
+          pair_publish();
+        }
         mfma_part(1);
       }
       // O (with PV(t-1) added) moves to tile t's reference max
@@ -1398,7 +1410,7 @@ __global__ __launch_bounds__(Duo<D>::THREADS, Duo<D>::PER_CU) void varlen_prefil
       __builtin_amdgcn_s_setprio(0);
       wait_vm_lgkm0<0>();
       if constexpr (kPairSync) {
-        pair_sync();
+        pair_wait();
       } else {
         bare_barrier();
       }
