@@ -1722,7 +1722,8 @@ struct Piece { int work, w0, w1; };
 // XCD w % kXcds), so its K and V stay in those XCDs' L2. An item costs its key tiles plus kItemOverhead for its
 // prologue and epilogue: a workgroup's extra single-tile item takes about as long as five
 // 64-key steps, and counting 8 balances best (config-3 batch 31.5 us against 32.2 us with
-// 3, 31.8 with 12, 32.9 with 16; batches of equal or mid-length segments unchanged). At
+// 3, 31.8 with 12, 32.9 with 16; batches of equal or mid-length segments unchanged;
+// rechecked on the current kernel: 28.2 us with 8 or 9, 28.9 with 5-7, 28.55 with 10). At
 // head_dim 256 (one workgroup per CU, ~1.15 us steps, ~6 us per item's ends) 5: config-3
 // lengths 40.3 us against 42.0 with 8, 40.8 with 2, 44.1 with 1 and 11, 40.2-40.4 with 3-6.
 int duo_schedule(const int32_t* cu, const std::vector<Piece>& pieces, const std::vector<Piece>& merges,
