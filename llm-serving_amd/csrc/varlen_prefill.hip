@@ -85,6 +85,21 @@ __device__ __forceinline__ floatx16 mfma32(const uint4& a, const uint4& b, const
 
 // Two fp32 values -> one word of two 16-bit values, round to nearest even; one
 // v_cvt_pk_bf16_f32 on gfx950 for bf16.
+// acc + lo + hi of one packed word of two 16-bit values, in one v_dot2 against (1, 1):
+// the row sum of the probabilities as rounded for the PV MFMA.
+template <typename T>
+__device__ __forceinline__ float sum_pair(uint32_t w, float acc) {
+  if constexpr (std::is_same<T, bf16_t>::value) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w),
+                                           __builtin_bit_cast(bf16x2_t, 0x3F803F80u), acc, false);
+  } else {
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, w), __builtin_bit_cast(f16x2_t, 0x3C003C00u),
+                                  acc, false);
+  }
+}
+
 template <typename T>
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
   if constexpr (std::is_same<T, bf16_t>::value) {
@@ -1342,14 +1357,8 @@ __global__ __launch_bounds__(Duo<D>::THREADS, Duo<D>::PER_CU) void varlen_prefil
       const float m_use = m_new == -INFINITY ? 0.0f : m_new;
       const float alpha = fast_exp2(m_i - m_use);
       m_i = m_new;
-      float lsum = 0.0f;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float p = fast_exp2(fmaf(sc[e], scale_log2, -m_use));
-        sc[e] = p;
-        lsum += p;
-      }
-      l_i = fmaf(l_i, alpha, lsum);
+      for (int e = 0; e < 16; ++e) sc[e] = fast_exp2(fmaf(sc[e], scale_log2, -m_use));
       // P(t) packed here, in the block of this step's MFMAs, and pinned: left alone the
       // compiler sinks the exponentials past the end of the step, beside the PV MFMAs that
       // read P, where nothing hides them (2-3% of the kernel)
@@ -1361,6 +1370,21 @@ __global__ __launch_bounds__(Duo<D>::THREADS, Duo<D>::PER_CU) void varlen_prefil
       }
       asm volatile("" : "+v"(pN[0].x), "+v"(pN[0].y), "+v"(pN[0].z), "+v"(pN[0].w),
                         "+v"(pN[1].x), "+v"(pN[1].y), "+v"(pN[1].z), "+v"(pN[1].w));
+      // the row sum is taken from the packed P, 8 dot2 in place of 16 adds, so that the
+      // fp32 probabilities die at the pack (summed from them, they stayed live across the
+      // step's MFMAs: 40.4 against 38.0 us at head_dim 256), and l sums the same rounded
+      // values that the PV MFMA weights V by
+      {
+        float ls = l_i * alpha;
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2) {
+          ls = sum_pair<T>(pN[t2].x, ls);
+          ls = sum_pair<T>(pN[t2].y, ls);
+          ls = sum_pair<T>(pN[t2].z, ls);
+          ls = sum_pair<T>(pN[t2].w, ls);
+        }
+        l_i = ls;
+      }
       floatx16 nxt = zero16();
       auto mfma_part = [&](int hf) {
 #pragma unroll
