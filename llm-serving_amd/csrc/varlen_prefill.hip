@@ -760,19 +760,21 @@ __global__ __launch_bounds__(Ring<D>::THREADS, 1) void varlen_prefill_ring_kerne
       const float m_use = m_new == -INFINITY ? 0.0f : m_new;
       alpha[j] = fast_exp2(m_i[j] - m_use);
       m_i[j] = m_new;
-      float lsum = 0.0f;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float p = fast_exp2(fmaf(sc[e], scale_log2, -m_use));
-        sc[e] = p;
-        lsum += p;
-      }
-      l_i[j] = fmaf(l_i[j], alpha[j], lsum);
+      for (int e = 0; e < 16; ++e) sc[e] = fast_exp2(fmaf(sc[e], scale_log2, -m_use));
+      // the row sum from the packed P, as in the duo kernel (8192 tokens: 309.9 against
+      // 313.9 us)
+      float ls = l_i[j] * alpha[j];
 #pragma unroll
       for (int t2 = 0; t2 < 2; ++t2) {
         pB[j][t2] = make_uint4(pack2<T>(sc[8 * t2 + 0], sc[8 * t2 + 1]), pack2<T>(sc[8 * t2 + 2], sc[8 * t2 + 3]),
                                pack2<T>(sc[8 * t2 + 4], sc[8 * t2 + 5]), pack2<T>(sc[8 * t2 + 6], sc[8 * t2 + 7]));
+        ls = sum_pair<T>(pB[j][t2].x, ls);
+        ls = sum_pair<T>(pB[j][t2].y, ls);
+        ls = sum_pair<T>(pB[j][t2].z, ls);
+        ls = sum_pair<T>(pB[j][t2].w, ls);
       }
+      l_i[j] = ls;
     }
 #if MIATTN_RING_SCHED <= 1
     // LDS reads first (V^T operands, K fragments), some vector work to cover their latency,
