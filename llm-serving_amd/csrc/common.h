@@ -139,6 +139,18 @@ __device__ __forceinline__ float swap32(float x) {
   return __uint_as_float(__lane_id() < 32 ? r[1] : r[0]);
 }
 
+// max / sum of x over lanes i and i ^ 32: swapped with a copy of itself, the two results
+// of v_permlane32_swap hold x's low and high half in every lane, so one op combines them
+// (no lane select after the swap)
+__device__ __forceinline__ float max_halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 struct SumOp {
   __device__ __forceinline__ static float op(float a, float b) { return a + b; }
 };

@@ -358,7 +358,7 @@ __global__ __launch_bounds__(Tiles<D>::THREADS, D <= 128 && Tiles<D>::NKS == 2 ?
       float mloc = sacc[0];
 #pragma unroll
       for (int j = 1; j < 16; ++j) mloc = fmaxf(mloc, sacc[j]);
-      const float m_tile = fmaxf(mloc, swap32(mloc)) * scale_log2;
+      const float m_tile = max_halves(mloc) * scale_log2;
       const float m_new = fmaxf(m_i, m_tile);
       const float m_use = m_new == -INFINITY ? 0.0f : m_new;
       // Rescale the accumulators only when some lane's running max moved (a wave-wide
@@ -415,7 +415,7 @@ __global__ __launch_bounds__(Tiles<D>::THREADS, D <= 128 && Tiles<D>::NKS == 2 ?
 
   // Fold the NKS key splits of each query block: the waves with kh > 0 publish
   // (m, l, O^T) through LDS, the kh = 0 waves merge, normalise and store.
-  const float l_tot = l_i + swap32(l_i);
+  const float l_tot = sum_halves(l_i);
   constexpr int NE = DB * 16 + 2;
   float* mbuf = reinterpret_cast<float*>(lds);  // [qb][kh-1][NE][64]
   if (kh > 0) {
@@ -750,7 +750,7 @@ __global__ __launch_bounds__(Ring<D>::THREADS, 1) void varlen_prefill_ring_kerne
       float mloc = sc[0];
 #pragma unroll
       for (int e = 1; e < 16; ++e) mloc = fmaxf(mloc, sc[e]);
-      const float m_tile = fmaxf(mloc, swap32(mloc)) * scale_log2;
+      const float m_tile = max_halves(mloc) * scale_log2;
       // Lazy rescaling: the reference max moves only when some query's tile max exceeds
       // it by more than 2^8 (log2 units); until then p = 2^(s - m) stays <= 256, exact to
       // the same relative precision in fp32 and in the 16-bit P operand, and O and l keep
@@ -900,7 +900,7 @@ __global__ __launch_bounds__(Ring<D>::THREADS, 1) void varlen_prefill_ring_kerne
 #pragma unroll
   for (int j = 0; j < QPW; ++j) {
     const int qb = qp * QPW + j;
-    const float l_tot = l_i[j] + swap32(l_i[j]);
+    const float l_tot = sum_halves(l_i[j]);
     float* obuf = reinterpret_cast<float*>(qb < 2 ? st0 : st1) + (qb & 1) * (DB * 16 * 64);
     float* mlbuf = reinterpret_cast<float*>(st2) + qb * 2 * 64;
     if (kh > 0) {
@@ -1357,7 +1357,7 @@ __global__ __launch_bounds__(Duo<D>::THREADS, Duo<D>::PER_CU) void varlen_prefil
       float mloc = sc[0];
 #pragma unroll
       for (int e = 1; e < 16; ++e) mloc = fmaxf(mloc, sc[e]);
-      const float m_tile = fmaxf(mloc, swap32(mloc)) * scale_log2;
+      const float m_tile = max_halves(mloc) * scale_log2;
       const bool moved = __any(m_tile > m_i + 8.0f);
       const float m_new = moved ? fmaxf(m_i, m_tile) : m_i;
       const float m_use = m_new == -INFINITY ? 0.0f : m_new;
@@ -1507,7 +1507,7 @@ __global__ __launch_bounds__(Duo<D>::THREADS, Duo<D>::PER_CU) void varlen_prefil
     int ln = lane;
     asm volatile("" : "+v"(ln));
     const int e_col = ln & 31, e_g = ln >> 5;
-    const float l_tot = l_i + swap32(l_i);
+    const float l_tot = sum_halves(l_i);
     mlx[kh][qb][0][ln] = m_i;
     mlx[kh][qb][1][ln] = l_tot;
     static_assert(DB * 16 * 64 * 4 <= W::BUFB, "a query block's fold fits one V buffer");
