@@ -1405,9 +1405,13 @@ __global__ __launch_bounds__(Duo<D>::THREADS, Duo<D>::PER_CU) void varlen_prefil
       };
       mfma_part(0);
       if constexpr (NH != 1) {
-        // the first half's 16 MFMAs each followed by up to 8 vector instructions of the
-        // softmax (37.1 against 37.6 us at head_dim 256; 4: 37.9, 6: 37.7, 10: 37.2,
-        // 12: 37.2, 16: 39.2)
+        // the first half's K fragment reads, 20 vector instructions of the softmax while they
+        // land (28: 38.2 us), its V^T reads (37.4 against 37.6 us left free), then its 16 MFMAs each
+        // followed by up to 8 vector instructions (37.1 against 37.6 us at head_dim 256; 4:
+        // 37.9, 6: 37.7, 10: 37.2, 12: 37.2, 16: 39.2)
+        __builtin_amdgcn_sched_group_barrier(0x0100, KSH, 0);
+        __builtin_amdgcn_sched_group_barrier(0x0002, 20, 0);
+        __builtin_amdgcn_sched_group_barrier(0x0100, 4 * DBH, 0);
 #pragma unroll
         for (int i = 0; i < KSH + 2 * DBH; ++i) {
           __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);
