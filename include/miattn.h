@@ -247,14 +247,16 @@ int mi_paged_decode_noalloc(const void* q, const void* k_cache, const void* v_ca
  * mi_varlen_schedule (host only) cuts the packed batch into query tiles, splits the
  * longest causal tiles' key ranges into pieces when the launch underfills the chip, and
  * orders the pieces heaviest-first so the causal triangle does not leave a tail of long
- * tiles. By default head_dim 64/128 batches whose longest segment reaches 8192 tokens run
- * the LDS-ring kernel (128-row tiles), shorter ones the persistent duo kernel (64-row
- * tiles, two workgroups per CU, each working through its own item list), head_dim 256 the
- * duo kernel at one workgroup per CU; batches of more than 255 heads (beyond the duo
- * kernel's item word) run the ring kernel at head_dim 64/128 and the register-staged
- * kernel at 256. mi_varlen_schedule_for names the kernel instead (MI_PREFILL_*; the ring
- * kernel takes head_dim 64 and 128, the duo kernel 64, 128 and 256 with at most 255 heads,
- * the register-staged kernel all three). Layout of
+ * tiles. By default head_dim 64/128 batches whose longest segment reaches 1536 tokens run
+ * the tall kernel (below) when its schedule needs no split pieces; otherwise batches whose
+ * longest segment reaches 8192 tokens run the LDS-ring kernel (128-row tiles) and shorter
+ * ones the persistent duo kernel (64-row tiles, two workgroups per CU, each working through
+ * its own item list); head_dim 256 runs the duo kernel at one workgroup per CU; batches of
+ * more than 255 heads (beyond the duo kernel's item word) run the ring kernel at head_dim
+ * 64/128 and the register-staged kernel at 256. mi_varlen_schedule_for names the kernel
+ * instead (MI_PREFILL_*; the ring and tall kernels take head_dim 64 and 128, the duo
+ * kernel 64, 128 and 256 with at most 255 heads, the register-staged kernel all three).
+ * Layout of
  * the staged and ring schedules:
  * {n_work, n_merge, n_partials, layout}, then n_work work entries and n_merge merge
  * entries of two words each; the duo schedule is {n_workgroups, n_merge, n_partials,
@@ -266,8 +268,20 @@ int mi_paged_decode_noalloc(const void* q, const void* k_cache, const void* v_ca
  * mi_varlen_prefill.
  * Split pieces write (O, max, sum) partials into the caller's workspace of
  * mi_varlen_workspace_size() bytes (0 when nothing is split; 16-byte aligned); a second
- * launch on the same stream merges them. Calls sharing a workspace must be ordered. */
-enum { MI_PREFILL_AUTO = -1, MI_PREFILL_STAGED = 0, MI_PREFILL_RING = 1, MI_PREFILL_DUO = 3 };
+ * launch on the same stream merges them. Calls sharing a workspace must be ordered.
+ * MI_PREFILL_TALL (head_dim 64/128, at most 65535 heads) runs 128-row tiles in which each
+ * wave owns 32 query rows over every key of a step; the schedule cuts long tiles' key
+ * ranges into pieces that run at the same time on different workgroups and merges them in
+ * the same launch (no second launch): its workspace starts with one int32 counter per split
+ * tile x head (rounded up to 256 bytes), which must be zero before the first call (zero the
+ * workspace once when allocating it) and which every call leaves zero, then the partials.
+ * Its schedule is {n_workgroups, n_counters, n_partials, layout}, n_workgroups entries of
+ * eight words {first item word, item count, the first item's six words}, then the items of
+ * six words each.
+ * error_word (device int32, may be NULL): a launch whose bounded wait gave up stores a
+ * non-zero code there (see mi_prefill_wait_limit) and ends normally; its output is not valid.
+ * The caller reads and clears it when it chooses (no per-call host synchronisation). */
+enum { MI_PREFILL_AUTO = -1, MI_PREFILL_STAGED = 0, MI_PREFILL_RING = 1, MI_PREFILL_DUO = 3, MI_PREFILL_TALL = 4 };
 int mi_varlen_schedule(const int32_t* host_cu_seqlens, int n_seqs, int H, int H_kv,
                        int D, int causal, int32_t* host_schedule, int capacity);
 int mi_varlen_schedule_for(const int32_t* host_cu_seqlens, int n_seqs, int H, int H_kv,
@@ -278,7 +292,14 @@ int mi_varlen_prefill(const void* q, const void* k, const void* v, void* out,
                       int max_seqlen, const int32_t* schedule, int n_work, int n_merge,
                       int n_partials, int layout, int H, int H_kv, int D, float scale,
                       int causal, int dtype, void* workspace, size_t workspace_bytes,
-                      void* stream);
+                      int32_t* error_word, void* stream);
+/* Test hook of the kernels' bounded waits (a tall owner waiting for its producers, a
+ * head_dim 256 duo wave waiting for its partner): polls >= 0 sets how many polls a wait makes
+ * before it gives up (for launches from then on, process-wide; 0: every wait gives up at
+ * once); polls < 0 only queries. Returns the previous limit. A correct launch never comes
+ * near the default; a small limit forces the give-up path, whose launch still ends normally
+ * with its output not to be trusted and 1 (tall) or 2 (duo) in the error word. */
+int mi_prefill_wait_limit(int polls);
 
 #ifdef __cplusplus
 }

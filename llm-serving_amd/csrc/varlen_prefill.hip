@@ -54,6 +54,14 @@ constexpr int kSchedHeader = 4;
 // 42.0 against 31.7 us on the config-3 batch); the ring kernel's 128-row tiles are 2%
 // faster at 8192 and 4% at 16384 tokens.
 constexpr int kRingMinLen = 8192;
+// The tall kernel is chosen (head_dim 64/128) when the longest segment reaches this many
+// tokens and its schedule deals the batch out without splitting any tile: measured on
+// MI355X (H16/H_kv8/D128 bf16, causal), 8 x 1536 tokens 105.0 against 107.6 us for the duo
+// kernel, 8 x 2048 168.4 against 177.3, 4 x 4096 292.8 against 309.0, 8192 272.7 against
+// 295.4 (ring 305.9), 16384 1046.5 against 1134.3 (ring 1155.6); 16 x 1024 112.3 against
+// 110.1. Where its schedule has to split tiles to fill the chip (2 x 2048: 70.7 against
+// 47.1 us; the config-3 batch: 44.4 against 32.2) the other kernels stay the choice.
+constexpr int kTallMinLen = 1536;
 #ifndef MIATTN_PREFILL_SPLIT
 #define MIATTN_PREFILL_SPLIT 1
 #endif
@@ -524,6 +532,7 @@ struct Ring {
 };
 
 typedef __attribute__((address_space(3))) void lds_void_t;
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
 typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4_t lds_short4_t;
 
@@ -531,6 +540,12 @@ typedef __attribute__((address_space(3))) short4_t lds_short4_t;
 // [16l, 16l + 16) after `dst` (the wave-uniform address goes through M0).
 __device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t rsrc, lds_void_t* dst, int voffset) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, dst, 16, voffset, 0, 0, 0);
+}
+// the same with a wave-uniform byte offset in soffset (one lane-offset register serves
+// every load of a tile)
+__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t rsrc, lds_void_t* dst, int voffset,
+                                                  int soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, dst, 16, voffset, soffset, 0, 0);
 }
 
 // s_waitcnt with vmcnt = N and lgkmcnt = 0 (expcnt left alone; gfx9 encoding).
@@ -969,6 +984,14 @@ __global__ __launch_bounds__(Ring<D>::THREADS, 1) void varlen_prefill_ring_kerne
   }
 }
 
+// Error word codes the prefill kernels report (the first one wins; the host clears it).
+constexpr int kErrTallWait = 1;  // a tall owner gave up waiting for its producers
+constexpr int kErrPairWait = 2;  // a head_dim 256 duo wave gave up waiting for its partner
+
+__device__ __forceinline__ void report(int32_t* err, int code) {
+  if (err != nullptr) atomicCAS(err, 0, code);
+}
+
 // ---------------------------------------------------------------- duo kernel (D = 64, 128)
 // Persistent: the grid is two workgroups per CU, and each works through its own list of
 // items (a 64-row query tile, or a key-range piece of one, of one head), which the host
@@ -1026,7 +1049,7 @@ template <typename T, int D>
 __global__ __launch_bounds__(Duo<D>::THREADS, Duo<D>::PER_CU) void varlen_prefill_duo_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     T* __restrict__ out, const int32_t* __restrict__ sched, float* __restrict__ partials, int H, int H_kv,
-    int G, float scale_log2, int causal) {
+    int G, float scale_log2, int causal, int32_t* __restrict__ err, int spin_max) {
   using W = Duo<D>;
   constexpr int KS = D / 16;  // MFMA k-steps over D for S^T
   constexpr int DB = D / 32;  // 32-row blocks of D for O^T
@@ -1136,9 +1159,8 @@ __global__ __launch_bounds__(Duo<D>::THREADS, Duo<D>::PER_CU) void varlen_prefil
   // reads of the shared rows are done (the caller's wait, before the step's last MFMAs), a
   // wave publishes its step count in LDS (pair_publish); at the end of the step it waits
   // until its partner's count has caught up (pair_wait). Both waves of a pair run the same
-  // steps, so the counts meet; the wait gives up after kPairSpinMax polls (a broken count
-  // then shows as wrong output in the tests, never as a hang).
-  constexpr int kPairSpinMax = 1 << 20;
+  // steps, so the counts meet; the wait gives up after spin_max polls and reports that
+  // through the error word (the launch then ends normally, its output not to be trusted).
   __shared__ int pflag[W::WAVES];
   int gstep = 0;
   auto pair_publish = [&]() {
@@ -1149,11 +1171,13 @@ __global__ __launch_bounds__(Duo<D>::THREADS, Duo<D>::PER_CU) void varlen_prefil
   };
   auto pair_wait = [&]() {
     asm volatile("" ::: "memory");
-    for (int spin = 0; spin < kPairSpinMax; ++spin) {
-      const int seen = __builtin_amdgcn_readfirstlane(
+    int seen = 0;
+    for (int spin = 0; spin < spin_max; ++spin) {
+      seen = __builtin_amdgcn_readfirstlane(
           __hip_atomic_load(&pflag[wave ^ 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
       if (seen >= gstep) break;  // (polled without s_sleep: 43.7 against 46.3 us with it)
     }
+    if (seen < gstep && lane == 0) report(err, kErrPairWait);
     asm volatile("" ::: "memory");
   };
   if constexpr (kPairSync) {
@@ -1612,6 +1636,584 @@ __global__ __launch_bounds__(Duo<D>::THREADS, Duo<D>::PER_CU) void varlen_prefil
   }
 }
 
+// ------------------------------------------------------------------ tall kernel
+// Persistent kernel of 128-row items in which every wave owns 32 query rows over all 64
+// keys of a step: wave w takes query block w, computes S^T for both 32-key blocks of the
+// step and PV over its 64 keys, so no two waves share a query row and an item ends without
+// a key-half fold. Each K/V tile in LDS feeds 128 query rows (the duo kernel's feed 64)
+// and a batch has half as many items. Two workgroups per CU (two waves per SIMD).
+//
+// An item whose key range is longer than the schedule's cap is cut into pieces that run
+// on different workgroups at the same time. Every piece except the one holding the
+// diagonal (the owner) is a producer: it writes its (O, m, l) partial with device-scope
+// stores, waits for them to be acknowledged and bumps the item's counter. The owner, after
+// its own steps, waits until the counter reaches its producer count, folds the partials
+// into its state, writes the output and takes its count back off the counter, so every
+// counter is zero again when the launch ends. A workgroup's item list never has an owner
+// before a producer and a producer never waits, so every wait ends while the grid is
+// resident (one launch of at most two workgroups per CU); the wait is bounded all the
+// same, and a wait that gives up is reported through the error word.
+template <int D>
+struct Tall {
+  static constexpr int WAVES = 4;             // query blocks of 32 rows, one per wave
+  static constexpr int THREADS = 64 * WAVES;
+  static constexpr int PER_CU = 2;
+  static constexpr int BQ = 32 * WAVES;       // query rows per item
+  static constexpr int BK = 64;               // keys per step
+  static constexpr int ROWB = D * 2;          // bytes of one row of one head
+  static constexpr int NCH = D / 8;           // 16-byte chunks per row
+  static constexpr int BUFB = BK * ROWB;      // bytes of one K (or V) buffer
+  static constexpr int SEGS = BUFB / 1024;    // 1 KiB wave-wide loads per buffer
+  static constexpr int LPW = SEGS / WAVES;    // of them per wave
+  static constexpr int RPS = 1024 / ROWB;     // rows per wave-wide load
+  static constexpr int SWB = NCH >= 16 ? 4 : 3;
+  static constexpr int SW_PERIOD = 1 << SWB;
+  // wave-wide loads i and i + LOAD_PERIOD of a wave land rows a whole swizzle period apart,
+  // so their lane offsets differ by a constant
+  static constexpr int LOAD_PERIOD = (WAVES * RPS) % SW_PERIOD == 0 ? 1 : SW_PERIOD / (WAVES * RPS);
+  // {seq0, L, tile << 16 | head, t_first << 16 | t_end, role << 30 | n_prod << 24 | counter,
+  //  partial slot (a producer's own; an owner's first producer's)}
+  static constexpr int ITEM_WORDS = 6;
+  static constexpr int ENTRY_WORDS = 2 + ITEM_WORDS;  // {first item word, count, item 0's words}
+  // one piece's partial: O^T per query block as [block][16 groups of 4 head dims][64 lanes]
+  // float4 (the accumulator layout, so the owner reads back exactly what each lane wrote),
+  // then (m, l) per query row as [block][32 rows] float2
+  static constexpr int PART_O = BQ * D;
+  static constexpr int PART_FLOATS = PART_O + 2 * BQ;
+  static constexpr int ROLE_WHOLE = 0, ROLE_PRODUCER = 1, ROLE_OWNER = 2;
+  static_assert(D == 64 || D == 128, "tall kernel head dims");
+  static_assert(SEGS % WAVES == 0 && LPW % LOAD_PERIOD == 0 && (WAVES * RPS * LOAD_PERIOD) % SW_PERIOD == 0,
+                "whole loads per wave, the lane-offset pattern periodic in the loads");
+  static_assert(2 * BUFB == BQ * ROWB, "a Q tile fills the two V buffers");
+  static constexpr __host__ __device__ int sw(int r) {
+    return ((r & 3) << (SWB - 2)) | ((r >> 2) & ((1 << (SWB - 2)) - 1));
+  }
+};
+
+template <typename T, int D>
+__global__ __launch_bounds__(Tall<D>::THREADS, Tall<D>::PER_CU) void varlen_prefill_tall_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, T* __restrict__ out,
+    const int32_t* __restrict__ sched, int32_t* __restrict__ counters, float* __restrict__ partials,
+    int32_t* __restrict__ err, int H, int H_kv, int G, float scale_log2, int causal, int spin_max) {
+  using W = Tall<D>;
+  constexpr int KS = D / 16;  // MFMA k-steps over D for S^T
+  constexpr int DB = D / 32;  // 32-row blocks of D for O^T
+  constexpr int BK = W::BK, BQ = W::BQ, ROWB = W::ROWB, LPW = W::LPW;
+  // two K and two V buffers; the Q tile's rows 0-63 go to V buffer 0 and rows 64-127 to V
+  // buffer 1 (so do the staged output rows), which are separate arrays so that the compiler
+  // sees that a load into one never aliases a read of the other
+  __shared__ __align__(512) uint8_t kb0[W::BUFB];
+  __shared__ __align__(512) uint8_t kb1[W::BUFB];
+  __shared__ __align__(512) uint8_t vb0[W::BUFB];
+  __shared__ __align__(512) uint8_t vb1[W::BUFB];
+  static_assert(W::BUFB == 64 * ROWB && W::WAVES == 4, "a V buffer holds the rows of two query blocks");
+
+  asm volatile("" ::"s"(q), "s"(k), "s"(v), "s"(out));
+  asm volatile("" ::"s"(H), "s"(H_kv), "s"(G), "s"(scale_log2), "s"(causal));
+  const int32_t* entry = sched + kSchedHeader + W::ENTRY_WORDS * blockIdx.x;
+  int first = entry[0], count = entry[1];
+  int iw[W::ITEM_WORDS];
+#pragma unroll
+  for (int j = 0; j < W::ITEM_WORDS; ++j) iw[j] = entry[2 + j];
+  static_assert(W::ITEM_WORDS == 6, "the pin below names six item words");
+  asm volatile("" : "+s"(first), "+s"(count), "+s"(iw[0]), "+s"(iw[1]), "+s"(iw[2]), "+s"(iw[3]), "+s"(iw[4]),
+                    "+s"(iw[5]));
+  if (count <= 0) return;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 5;
+  const int col = lane & 31;
+  const int64_t q_row = int64_t(H) * D;
+  const int64_t q_row_b = q_row * int64_t(sizeof(T));
+  const int64_t kv_row_b = int64_t(H_kv) * ROWB;
+
+  struct Item {
+    int seq0, L, row0, h, t_first, t_end, role, n_prod, counter, slot;
+  };
+  auto load_words = [&](int i) {
+    const int32_t* w = sched + first + W::ITEM_WORDS * i;
+#pragma unroll
+    for (int j = 0; j < W::ITEM_WORDS; ++j) iw[j] = __builtin_amdgcn_readfirstlane(w[j]);
+  };
+  auto decode = [&]() {
+    Item it;
+    it.seq0 = iw[0];
+    it.L = iw[1];
+    it.row0 = int(uint32_t(iw[2]) >> 16) * BQ;
+    it.h = iw[2] & 0xffff;
+    it.t_first = int(uint32_t(iw[3]) >> 16);
+    it.t_end = iw[3] & 0xffff;
+    it.role = int(uint32_t(iw[4]) >> 30);
+    it.n_prod = (iw[4] >> 24) & 63;
+    it.counter = iw[4] & 0xffffff;
+    it.slot = iw[5];
+    return it;
+  };
+
+  // Load i of this wave fills 1 KiB segment wave + i * WAVES of a buffer: lane t writes
+  // bytes 16t.. of it, i.e. row (wave + i * WAVES) * RPS + t / NCH, slot t % NCH, which holds
+  // chunk slot ^ sw(row); sw repeats every LOAD_PERIOD loads, so load i is load i % LP
+  // shifted by (i / LP) * WAVES * RPS * LP rows (a scalar offset). One buffer resource per
+  // tile: base = the tile's first token at the item's KV head, range = the tile's rows inside
+  // the segment (rows past it read as zero).
+  constexpr int LP = W::LOAD_PERIOD;
+  int dma_off[LP];
+#pragma unroll
+  for (int p = 0; p < LP; ++p) {
+    const int r = (wave + p * W::WAVES) * W::RPS + lane / W::NCH;
+    dma_off[p] = int(r * kv_row_b) + (((lane % W::NCH) ^ W::sw(r)) << 4);
+  }
+  const int dma_step = int(W::WAVES * W::RPS * LP * kv_row_b);
+  auto issue = [&](const char* seg, const Item& it, int t, uint8_t* dst) {
+    const int rows = t < it.t_end ? min(it.L - t * BK, BK) : 0;
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(seg + uint64_t(uint32_t(t)) * uint32_t(BK * kv_row_b)), (short)0, rows * int(kv_row_b),
+        0x00020000);
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+      buffer_load_lds16(rs, (lds_void_t*)((__attribute__((address_space(3))) uint8_t*)dst + (wave + i * W::WAVES) * 1024),
+                        dma_off[i % LP], (i / LP) * dma_step);
+    }
+  };
+  auto seg_of = [&](const T* base, const Item& it) {
+    return reinterpret_cast<const char*>(base) + int64_t(it.seq0) * kv_row_b + (it.h / G) * ROWB;
+  };
+  // The item's Q tile (128 rows, laid out like a K tile) fills both V buffers; rows past the
+  // segment read as zero. Lane offsets rebuilt per call from an opaque copy of the lane id.
+  auto issue_q = [&](const Item& it) {
+    int ql = lane;
+    asm volatile("" : "+v"(ql));
+    int off[LP];
+#pragma unroll
+    for (int p = 0; p < LP; ++p) {
+      const int r = (wave + p * W::WAVES) * W::RPS + ql / W::NCH;
+      off[p] = int(r * q_row_b) + (((ql % W::NCH) ^ W::sw(r)) << 4);
+    }
+    const int step_b = int(W::WAVES * W::RPS * LP * q_row_b);
+    const int rows = min(it.L - it.row0, BQ);
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(reinterpret_cast<const char*>(q) + int64_t(it.seq0 + it.row0) * q_row_b + it.h * ROWB),
+        (short)0, rows * int(q_row_b), 0x00020000);
+#pragma unroll
+    for (int i = 0; i < 2 * LPW; ++i) {
+      // segment wave + i * WAVES of the tile: V buffer 0 holds the first SEGS, buffer 1 the rest
+      uint8_t* dst = i < LPW ? vb0 : vb1;
+      buffer_load_lds16(rs, (lds_void_t*)((__attribute__((address_space(3))) uint8_t*)dst + (wave + (i % LPW) * W::WAVES) * 1024),
+                        off[i % LP], (i / LP) * step_b);
+    }
+  };
+  // this wave's query rows (wave * 32 .. +31 of the item) in a Q tile or a staged output:
+  // V buffer wave >> 1
+  uint8_t* const qrows = (wave < 2 ? vb0 : vb1) + (wave & 1) * 32 * ROWB;
+
+  // LDS byte offsets of this lane's operands, derived per read from three bases (eight
+  // K and eight V offsets held in registers push the four-wave kernel into spills): the K
+  // (and Q) fragment of k-step ks of a 32-row block is chunk (2 ks + g) ^ sw(row) =
+  // (g ^ sw(row)) ^ 2 ks of its row, i.e. kx ^ (ks << 5), block b b * 32 rows on (sw depends
+  // on the row mod SW_PERIOD, which divides 32); the two transposed reads of V^T block db
+  // are chunks (4 db + x) ^ sw(key) = (x ^ sw(key)) ^ 4 db, i.e. vx[hh] ^ (db << 6), and
+  // 16-key k-step s4 sits 16 s4 rows on. The bases pass through an empty asm at each step
+  // (otherwise the compiler hoists every XORed offset out of the loop and spills them).
+  static_assert(ROWB % 256 == 0 || (ROWB == 128 && KS == 4 && DB == 2), "XOR offsets: chunk bits free of row bits");
+  const int kx0 = col * ROWB + ((g ^ W::sw(col)) << 4);
+  int vx0[2];
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    const int key = 8 * hh + 4 * g + ((lane & 15) >> 2);
+    const int d0 = ((lane >> 4) & 1) * 16 + 4 * (lane & 3);
+    vx0[hh] = key * ROWB + (((d0 >> 3) ^ W::sw(key)) << 4) + ((d0 >> 2) & 1) * 8;
+  }
+  int kx = kx0, vx[2] = {vx0[0], vx0[1]};
+  auto fresh_bases = [&]() {
+    kx = kx0;
+    vx[0] = vx0[0];
+    vx[1] = vx0[1];
+    asm volatile("" : "+v"(kx), "+v"(vx[0]), "+v"(vx[1]));
+  };
+  auto koff = [&](int ks) { return kx ^ (ks << 5); };
+  static_assert(W::sw(16) == W::sw(0) && W::sw(32) == W::sw(0), "16- and 32-row shifts keep the swizzle");
+
+  auto read_vt = [&](const uint8_t* vb, int db, int s4) {
+    const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_short4_t*)((__attribute__((address_space(3))) const uint8_t*)vb + (vx[0] ^ (db << 6)) + s4 * 16 * ROWB));
+    const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_short4_t*)((__attribute__((address_space(3))) const uint8_t*)vb + (vx[1] ^ (db << 6)) + s4 * 16 * ROWB));
+    const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+    return make_uint4(l2.x, l2.y, h2.x, h2.y);
+  };
+
+  // first item: Q, K(t0) and K(t0+1) in flight (later items get them from the previous
+  // item's last step and epilogue)
+  Item it = decode();
+  const char* kseg = seg_of(k, it);
+  const char* vseg = seg_of(v, it);
+  issue_q(it);
+  issue(kseg, it, it.t_first, kb0);
+  issue(kseg, it, it.t_first + 1, kb1);
+  uint4 qB[KS];
+  constexpr int RPI = 64 / W::NCH;       // rows per wave-wide 16-byte read of the staged output
+  constexpr int kStores = 32 / RPI;     // output stores per wave per item
+  bool stored = false;                   // the previous item left its output stores in flight
+
+  for (int idx = 0; idx < count; ++idx) {
+    const int L = it.L;
+    const int n_it = it.t_end - it.t_first;
+    const bool more = idx + 1 < count;
+    if (more) load_words(idx + 1);
+    // Q, K(t0), K(t0+1) landed. A whole or owner item before this one issued its output
+    // stores after this item's Q loads, always kStores of them (range-checked, so rows past
+    // the segment are dropped, not skipped): vmcnt(kStores) leaves them in flight.
+    if (stored) {
+      wait_vm_lgkm0<kStores>();
+    } else {
+      wait_vm_lgkm0<0>();
+    }
+    bare_barrier();
+    floatx16 cur[2];
+    {
+      fresh_bases();
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) qB[ks] = *reinterpret_cast<const uint4*>(qrows + koff(ks));
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        uint4 kf[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) kf[ks] = *reinterpret_cast<const uint4*>(kb0 + b * 32 * ROWB + koff(ks));
+        cur[b] = zero16();
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) cur[b] = mfma32<T>(kf[ks], qB[ks], cur[b]);
+      }
+    }
+    wait_lgkm0();
+    bare_barrier();  // Q and K(t0) read by every wave: the V buffers and K buffer 0 are free
+
+    floatx16 o[DB];
+#pragma unroll
+    for (int i = 0; i < DB; ++i) o[i] = zero16();
+    float m_i = -INFINITY, l_i = 0.0f;
+    uint4 pB[4];  // P of the previous tile (4 k-steps of 16 keys), whose PV runs in this step
+
+    // Step sidx (tile t = t_first + sidx): softmax of tile t (scores in cur), the scores of
+    // tile t+1 (K(t+1) in kb_next; kS) and PV of tile t-1 (V(t-1) in vb_prev; kPV), so every
+    // MFMA of the step is independent of the step's softmax; K(t+2) goes to kb_free and V(t)
+    // to vb_free. The last step of an item computes no scores; instead it starts the next
+    // item's first two K tiles (both K buffers are free: K(t) was read in the step before).
+    auto step = [&](int sidx, const uint8_t* kb_next, uint8_t* kb_free, const uint8_t* vb_prev, uint8_t* vb_free,
+                    auto pv_c, auto s_c, const Item& nx, const char* nkseg) {
+      constexpr bool kPV = decltype(pv_c)::value;
+      constexpr bool kS = decltype(s_c)::value;
+      const int t = it.t_first + sidx;
+      issue(vseg, it, t, vb_free);
+      if constexpr (kS) {
+        if (t + 2 < it.t_end) issue(kseg, it, t + 2, kb_free);
+      } else {
+        if (more) {
+          issue(nkseg, nx, nx.t_first, kb0);
+          issue(nkseg, nx, nx.t_first + 1, kb1);
+        }
+      }
+      __builtin_amdgcn_s_setprio(1);
+      fresh_bases();
+      floatx16 sc[2] = {cur[0], cur[1]};
+      // only a tile that reaches past the segment end or the item's first row needs the mask
+      if ((t + 1) * BK > L || (causal && (t + 1) * BK - 1 > it.row0)) {
+        const int qi = it.row0 + wave * 32 + col;
+        const int lim0 = (causal ? min(L, qi + 1) : L) - t * BK - g * 4;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          const int lim = lim0 - b * 32;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            if ((e >> 2) * 8 + (e & 3) >= lim) sc[b][e] = -INFINITY;
+          }
+        }
+      }
+      // Phase A: PV(t-1) on the matrix cores (four groups of four MFMAs, one per 16-key
+      // k-step, each group's V^T operands read during the group before) while the row max
+      // of tile t is formed. Phase B: the scores of tile t+1 (eight groups of two MFMAs, K
+      // operands read a group ahead) while tile t's exponentials are taken, packed to 16
+      // bits (the next step's PV operand) and summed. sched_barrier keeps each group's reads
+      // ahead of the group before's MFMAs.
+      float mx[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) mx[j] = fmaxf(fmaxf(sc[0][4 * j], sc[0][4 * j + 1]), fmaxf(sc[0][4 * j + 2], sc[0][4 * j + 3]));
+      uint4 fa[DB], fb[DB];
+      if constexpr (kPV) {
+#pragma unroll
+        for (int db = 0; db < DB; ++db) fa[db] = read_vt(vb_prev, db, 0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+          if (s4 + 1 < 4) {
+#pragma unroll
+            for (int db = 0; db < DB; ++db) fb[db] = read_vt(vb_prev, db, s4 + 1);
+          }
+#pragma unroll
+          for (int db = 0; db < DB; ++db) o[db] = mfma32<T>(fa[db], pB[s4], o[db]);
+          // a quarter of the row max's vector work between this group's MFMAs
+#pragma unroll
+          for (int j = 0; j < 4; ++j) mx[j] = fmaxf(mx[j], sc[1][4 * s4 + j]);
+          if (s4 + 1 < 4) __builtin_amdgcn_sched_group_barrier(0x0100, 2 * DB, 0);
+#pragma unroll
+          for (int db = 0; db < DB; ++db) {
+            __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x0002, 2, 0);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int db = 0; db < DB; ++db) fa[db] = fb[db];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mx[e & 3] = fmaxf(mx[e & 3], sc[1][e]);
+      }
+      const float mloc = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
+      const float m_tile = max_halves(mloc) * scale_log2;
+      const bool moved = __any(m_tile > m_i + 8.0f);
+      const float m_new = moved ? fmaxf(m_i, m_tile) : m_i;
+      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+      const float alpha = fast_exp2(m_i - m_use);
+      m_i = m_new;
+      float ls = l_i * alpha;
+      // phase B, group q (of NG): K operands of group q+1 read, group q's PG MFMAs, and its
+      // share of the exponentials (EPG of them, part of P's k-step (q * EPG) / 8)
+      constexpr int PG = 2;                 // MFMAs per group
+      constexpr int NG = 2 * KS / PG;       // groups
+      constexpr int EPG = 32 / NG;          // exponentials per group
+      uint4 ka[PG], kn[PG];
+      if constexpr (kS) {
+#pragma unroll
+        for (int i = 0; i < PG; ++i) ka[i] = *reinterpret_cast<const uint4*>(kb_next + koff(i));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      floatx16 acc[2];
+      float p8[8];
+#pragma unroll
+      for (int qg = 0; qg < NG; ++qg) {
+        const int b = (qg * PG) / KS, k0 = (qg * PG) % KS;
+        if constexpr (kS) {
+          if (qg + 1 < NG) {
+            const int b1 = ((qg + 1) * PG) / KS, k1 = ((qg + 1) * PG) % KS;
+#pragma unroll
+            for (int i = 0; i < PG; ++i) kn[i] = *reinterpret_cast<const uint4*>(kb_next + b1 * 32 * ROWB + koff(k1 + i));
+          }
+          if (k0 == 0) acc[b] = zero16();
+#pragma unroll
+          for (int i = 0; i < PG; ++i) acc[b] = mfma32<T>(ka[i], qB[k0 + i], acc[b]);
+        }
+        const int s4 = (qg * EPG) / 8, j0 = (qg * EPG) % 8;
+        const floatx16& src = sc[s4 >> 1];
+#pragma unroll
+        for (int j = 0; j < EPG; ++j) p8[j0 + j] = fast_exp2(fmaf(src[8 * (s4 & 1) + j0 + j], scale_log2, -m_use));
+        if (j0 + EPG == 8) {
+          pB[s4] = make_uint4(pack2<T>(p8[0], p8[1]), pack2<T>(p8[2], p8[3]), pack2<T>(p8[4], p8[5]),
+                              pack2<T>(p8[6], p8[7]));
+          // pinned here, in this group: left alone the compiler sinks the exponentials into
+          // the next step, beside the PV MFMAs that read P
+          asm volatile("" : "+v"(pB[s4].x), "+v"(pB[s4].y), "+v"(pB[s4].z), "+v"(pB[s4].w));
+          ls = sum_pair<T>(pB[s4].x, ls);
+          ls = sum_pair<T>(pB[s4].y, ls);
+          ls = sum_pair<T>(pB[s4].z, ls);
+          ls = sum_pair<T>(pB[s4].w, ls);
+        }
+        if constexpr (kS) {
+          if (qg + 1 < NG) __builtin_amdgcn_sched_group_barrier(0x0100, PG, 0);
+#pragma unroll
+          for (int i = 0; i < PG; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x0002, 4, 0);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < PG; ++i) ka[i] = kn[i];
+      }
+      l_i = ls;
+      if constexpr (kS) {
+        cur[0] = acc[0];
+        cur[1] = acc[1];
+      }
+      // O (with PV(t-1) added) moves to tile t's reference max
+      if (moved) {
+#pragma unroll
+        for (int i = 0; i < DB; ++i) o[i] *= alpha;
+      }
+      __builtin_amdgcn_s_setprio(0);
+      wait_vm_lgkm0<0>();
+      bare_barrier();
+    };
+    auto drain = [&](const uint8_t* vb) {
+      fresh_bases();
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+#pragma unroll
+        for (int db = 0; db < DB; ++db) o[db] = mfma32<T>(read_vt(vb, db, s4), pB[s4], o[db]);
+      }
+    };
+    const Item cur_it = it;
+    Item nx = it;
+    const char* nkseg = kseg;
+    if (more) {
+      nx = decode();
+      nkseg = seg_of(k, nx);
+    }
+    using No = std::false_type;
+    using Yes = std::true_type;
+    if (n_it == 1) {
+      step(0, kb1, kb0, vb1, vb0, No{}, No{}, nx, nkseg);
+      drain(vb0);
+    } else {
+      step(0, kb1, kb0, vb1, vb0, No{}, Yes{}, nx, nkseg);
+      int sidx = 1;
+      for (; sidx + 2 < n_it; sidx += 2) {
+        step(sidx, kb0, kb1, vb0, vb1, Yes{}, Yes{}, nx, nkseg);
+        step(sidx + 1, kb1, kb0, vb1, vb0, Yes{}, Yes{}, nx, nkseg);
+      }
+      if (sidx + 1 < n_it) {
+        step(sidx, kb0, kb1, vb0, vb1, Yes{}, Yes{}, nx, nkseg);
+        ++sidx;
+      }
+      // sidx == n_it - 1: the last step, then PV of the last tile (V in buffer sidx & 1)
+      if (sidx & 1) {
+        step(sidx, kb0, kb1, vb0, vb1, Yes{}, No{}, nx, nkseg);
+        drain(vb1);
+      } else {
+        step(sidx, kb1, kb0, vb1, vb0, Yes{}, No{}, nx, nkseg);
+        drain(vb0);
+      }
+    }
+    it = nx;
+    kseg = nkseg;
+    vseg = seg_of(v, it);
+
+    // ---- epilogue of cur_it
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int e_col = ln & 31, e_g = ln >> 5;
+    float l_tot = sum_halves(l_i);
+    // this wave's slice of a piece's partial
+    auto part_rsrc = [&](int slot) {
+      return __builtin_amdgcn_make_buffer_rsrc(partials + int64_t(slot) * W::PART_FLOATS, (short)0,
+                                               W::PART_FLOATS * 4, 0x00020000);
+    };
+    constexpr int kSc1 = 16;  // device-scope cache policy: written through / read from the coherent level
+    if (cur_it.role == W::ROLE_PRODUCER) {
+      const auto rs = part_rsrc(cur_it.slot);
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int grp = db * 4 + j;
+          const u32x4_nt val = {__float_as_uint(o[db][4 * j + 0]), __float_as_uint(o[db][4 * j + 1]),
+                                __float_as_uint(o[db][4 * j + 2]), __float_as_uint(o[db][4 * j + 3])};
+          __builtin_amdgcn_raw_buffer_store_b128(val, rs, ((wave * (DB * 4) + grp) * 64 + ln) * 16, 0, kSc1);
+        }
+      }
+      if (e_g == 0) {
+        const u32x2_t ml = {__float_as_uint(m_i), __float_as_uint(l_tot)};
+        __builtin_amdgcn_raw_buffer_store_b64(ml, rs, (W::PART_O + (wave * 32 + e_col) * 2) * 4, 0, kSc1);
+      }
+      stored = false;
+      wait_vm_lgkm0<0>();  // this wave's partial is at the coherent level
+      bare_barrier();      // ... and every wave's
+      if (tid == 0) __hip_atomic_fetch_add(counters + cur_it.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      if (cur_it.role == W::ROLE_OWNER) {
+        // wait for the producers' count (bounded), then fold each partial in
+        int seen = 0;
+        for (int spin = 0; spin < spin_max; ++spin) {
+          seen = __builtin_amdgcn_readfirstlane(
+              __hip_atomic_load(counters + cur_it.counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+          if (seen >= cur_it.n_prod) break;
+          __builtin_amdgcn_s_sleep(2);
+        }
+        if (seen < cur_it.n_prod && ln == 0) report(err, kErrTallWait);
+        for (int p = 0; p < cur_it.n_prod; ++p) {
+          const auto rs = part_rsrc(cur_it.slot + p);
+          const u32x2_t ml = __builtin_amdgcn_raw_buffer_load_b64(rs, (W::PART_O + (wave * 32 + e_col) * 2) * 4, 0, kSc1);
+          u32x4_nt po[DB * 4];
+#pragma unroll
+          for (int grp = 0; grp < DB * 4; ++grp) {
+            po[grp] = __builtin_amdgcn_raw_buffer_load_b128(rs, ((wave * (DB * 4) + grp) * 64 + ln) * 16, 0, kSc1);
+          }
+          const float m_p = __uint_as_float(ml.x), l_p = __uint_as_float(ml.y);
+          const float M = fmaxf(m_i, m_p);
+          const float M_use = M == -INFINITY ? 0.0f : M;
+          const float w_me = fast_exp2(m_i - M_use);
+          const float w_p = fast_exp2(m_p - M_use);
+          l_tot = fmaf(l_p, w_p, l_tot * w_me);
+          m_i = M;
+#pragma unroll
+          for (int db = 0; db < DB; ++db) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const u32x4_nt pv = po[db * 4 + j];
+              o[db][4 * j + 0] = fmaf(__uint_as_float(pv.x), w_p, o[db][4 * j + 0] * w_me);
+              o[db][4 * j + 1] = fmaf(__uint_as_float(pv.y), w_p, o[db][4 * j + 1] * w_me);
+              o[db][4 * j + 2] = fmaf(__uint_as_float(pv.z), w_p, o[db][4 * j + 2] * w_me);
+              o[db][4 * j + 3] = fmaf(__uint_as_float(pv.w), w_p, o[db][4 * j + 3] * w_me);
+            }
+          }
+        }
+      }
+      const float inv = 1.0f / fmaxf(l_tot, 1e-30f);
+      // every wave has read the last V tile: the V buffers take the staged output
+      wait_lgkm0();
+      bare_barrier();
+      if (cur_it.role == W::ROLE_OWNER && tid == 0) {
+        // every wave has seen the count: take it back off (a producer that arrives after a
+        // give-up leaves the counter at zero too)
+        __hip_atomic_fetch_add(counters + cur_it.counter, -cur_it.n_prod, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      // staged as [row][16-byte chunk c at c ^ (row % NCH)] in this wave's 32 rows of the V
+      // buffers, then read back 16 bytes per lane along the rows and stored as whole lines
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int c = db * 4 + j;
+          float* f = reinterpret_cast<float*>(qrows + e_col * ROWB + ((c ^ (e_col & (W::NCH - 1))) << 4) + e_g * 8);
+          f[0] = __builtin_bit_cast(float, pack2<T>(o[db][4 * j + 0] * inv, o[db][4 * j + 1] * inv));
+          f[1] = __builtin_bit_cast(float, pack2<T>(o[db][4 * j + 2] * inv, o[db][4 * j + 3] * inv));
+        }
+      }
+      wait_lgkm0();
+      uint4 val[kStores];
+#pragma unroll
+      for (int i = 0; i < kStores; ++i) {
+        const int rr = i * RPI + ln / W::NCH;
+        const int c = ln % W::NCH;
+        val[i] = *reinterpret_cast<const uint4*>(qrows + rr * ROWB + ((c ^ (rr & (W::NCH - 1))) << 4));
+      }
+      wait_lgkm0();
+      bare_barrier();  // every wave has read its staged rows: the V buffers take the next Q
+      if (more) issue_q(it);
+      // the output stores go after the next item's Q loads, so the wait for Q does not wait
+      // for them; one resource over the item's rows inside the segment, so the stores of rows
+      // past it are dropped by the range check and every wave issues exactly kStores
+      {
+        const auto rs = __builtin_amdgcn_make_buffer_rsrc(
+            reinterpret_cast<char*>(out) + int64_t(cur_it.seq0 + cur_it.row0) * q_row_b + cur_it.h * ROWB, (short)0,
+            min(cur_it.L - cur_it.row0, BQ) * int(q_row_b), 0x00020000);
+        constexpr int kNt = 2;  // nontemporal: the output is not read again by this kernel
+#pragma unroll
+        for (int i = 0; i < kStores; ++i) {
+          const int rr = i * RPI + ln / W::NCH;
+          const int c = ln % W::NCH;
+          const u32x4_nt w = {val[i].x, val[i].y, val[i].z, val[i].w};
+          __builtin_amdgcn_raw_buffer_store_b128(w, rs, (wave * 32 + rr) * int(q_row_b) + c * 16, 0, kNt);
+        }
+      }
+      stored = true;
+      continue;
+    }
+    // producer: the V buffers are free once every wave has passed the barrier above
+    if (more) issue_q(it);
+  }
+}
+
 // Second launch for split query tiles, one workgroup per (head, merge entry, quarter of
 // the tile's rows); each thread owns 32 columns of one row and folds that row over the
 // pieces (log-sum-exp on the stored (M, l)), with every load of all pieces in flight at
@@ -1680,28 +2282,61 @@ __global__ __launch_bounds__(256) void varlen_prefill_merge_kernel(
 }
 
 // Schedule layout word: kernel kind << 20 | head_dim << 8 | query rows per tile.
-enum Kind { kStaged = MI_PREFILL_STAGED, kRing = MI_PREFILL_RING, kDuo = MI_PREFILL_DUO };
+enum Kind { kStaged = MI_PREFILL_STAGED, kRing = MI_PREFILL_RING, kDuo = MI_PREFILL_DUO, kTall = MI_PREFILL_TALL };
 constexpr int layout_word(int kind, int D, int rows) { return (kind << 20) | (D << 8) | rows; }
 constexpr int layout_kind(int layout) { return layout >> 20; }
 constexpr int layout_d(int layout) { return (layout >> 8) & 0xfff; }
 constexpr int layout_rows(int layout) { return layout & 0xff; }
 int kind_rows(int kind) {
-  return kind == kRing ? Ring<128>::BQ : kind == kDuo ? Duo<128>::BQ : kBQ;
+  return kind == kRing ? Ring<128>::BQ : kind == kDuo ? Duo<128>::BQ : kind == kTall ? Tall<128>::BQ : kBQ;
 }
 // keys per schedule unit of work (a causal tile's cost is counted in these)
-int kind_keys(int kind) { return kind == kDuo ? Duo<128>::BK : Ring<128>::BK; }
+int kind_keys(int kind) { return kind == kDuo ? Duo<128>::BK : kind == kTall ? Tall<128>::BK : Ring<128>::BK; }
 // workgroups one CU holds at once
 int kind_per_cu(int kind, int D) {
-  return kind == kDuo ? (D == 256 ? Duo<256>::PER_CU : Duo<128>::PER_CU) : kind == kStaged ? 2 : 1;
+  return kind == kDuo ? (D == 256 ? Duo<256>::PER_CU : Duo<128>::PER_CU)
+         : kind == kTall ? Tall<128>::PER_CU : kind == kStaged ? 2 : 1;
 }
 static_assert(Ring<128>::BK == Tiles<256>::BK && Ring<64>::BK == Tiles<128>::BK, "64-key tiles");
 static_assert(Duo<64>::BQ == Duo<128>::BQ && Duo<64>::BK == Duo<128>::BK, "duo tile shape");
+static_assert(Tall<64>::BQ == Tall<128>::BQ && Tall<64>::BK == Tall<128>::BK &&
+                  Tall<64>::ITEM_WORDS == Tall<128>::ITEM_WORDS, "tall tile shape");
+
+// Polls a bounded wait makes before it gives up (a tall owner waiting for its producers, a
+// head_dim 256 duo wave waiting for its partner): set by mi_prefill_wait_limit, read at each
+// launch. Each tall poll sleeps ~0.1 us, so the default bounds a wait at ~0.1 s, far beyond
+// any wait a correct launch makes (at most one producer piece's run time).
+int g_wait_limit = 1 << 20;
+
+// Bytes of the tall kernel's workspace ahead of the partials: one int32 counter per split
+// item, rounded up to 256 bytes. They must be zero before the first launch; every launch
+// leaves them zero.
+size_t tall_counter_bytes(int n_counters) { return (size_t(n_counters) * 4 + 255) / 256 * 256; }
+size_t tall_workspace_bytes(int n_counters, int n_partials, int D) {
+  if (n_partials == 0) return 0;
+  const size_t per = size_t(D == 64 ? Tall<64>::PART_FLOATS : Tall<128>::PART_FLOATS) * sizeof(float);
+  return tall_counter_bytes(n_counters) + size_t(n_partials) * per;
+}
 
 template <typename T, int D>
 int launch2(const void* q, const void* k, const void* v, void* out, const int32_t* cu,
-            const int32_t* sched, int n_work, int n_merge, int kind, float* partials, int H,
-            int H_kv, float scale_log2, int causal, hipStream_t s) {
+            const int32_t* sched, int n_work, int n_merge, int kind, void* workspace, int H,
+            int H_kv, float scale_log2, int causal, int32_t* err, hipStream_t s) {
   const int32_t* work = sched + kSchedHeader;
+  float* partials = static_cast<float*>(workspace);
+  if constexpr (D == 64 || D == 128) {
+    if (kind == kTall) {
+      // n_merge holds the split items' counter count; the counters lead the workspace
+      int32_t* counters = static_cast<int32_t*>(workspace);
+      float* tall_partials = workspace == nullptr ? nullptr
+          : reinterpret_cast<float*>(static_cast<char*>(workspace) + tall_counter_bytes(n_merge));
+      hipLaunchKernelGGL((varlen_prefill_tall_kernel<T, D>), dim3(n_work), dim3(Tall<D>::THREADS), 0, s,
+                         static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
+                         static_cast<T*>(out), sched, counters, tall_partials, err, H, H_kv, H / H_kv, scale_log2,
+                         causal, g_wait_limit);
+      return launch_status("mi_varlen_prefill");
+    }
+  }
   if constexpr (D == 64 || D == 128 || D == 256) {
     if (kind == kDuo || (D != 256 && kind == kRing)) {
       constexpr int kRowsPerBlock = 256 / (D / 32);
@@ -1721,7 +2356,8 @@ int launch2(const void* q, const void* k, const void* v, void* out, const int32_
         // follow the table
         hipLaunchKernelGGL((varlen_prefill_duo_kernel<T, D>), dim3(n_work), dim3(Duo<D>::THREADS), 0, s,
                            static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
-                           static_cast<T*>(out), sched, partials, H, H_kv, H / H_kv, scale_log2, causal);
+                           static_cast<T*>(out), sched, partials, H, H_kv, H / H_kv, scale_log2, causal, err,
+                           g_wait_limit);
         if (n_merge > 0) {
           hipLaunchKernelGGL((varlen_prefill_merge_kernel<T, D, Duo<D>::BQ>),
                              dim3(H, n_merge, (Duo<D>::BQ + kRowsPerBlock - 1) / kRowsPerBlock), dim3(256), 0, s,
@@ -1740,12 +2376,12 @@ int launch2(const void* q, const void* k, const void* v, void* out, const int32_
 
 template <typename T>
 int launch1(int D, const void* q, const void* k, const void* v, void* out, const int32_t* cu,
-            const int32_t* sched, int n_work, int n_merge, int kind, float* partials, int H,
-            int H_kv, float sl2, int causal, hipStream_t s) {
+            const int32_t* sched, int n_work, int n_merge, int kind, void* ws, int H,
+            int H_kv, float sl2, int causal, int32_t* err, hipStream_t s) {
   switch (D) {
-    case 64: return launch2<T, 64>(q, k, v, out, cu, sched, n_work, n_merge, kind, partials, H, H_kv, sl2, causal, s);
-    case 128: return launch2<T, 128>(q, k, v, out, cu, sched, n_work, n_merge, kind, partials, H, H_kv, sl2, causal, s);
-    case 256: return launch2<T, 256>(q, k, v, out, cu, sched, n_work, n_merge, kind, partials, H, H_kv, sl2, causal, s);
+    case 64: return launch2<T, 64>(q, k, v, out, cu, sched, n_work, n_merge, kind, ws, H, H_kv, sl2, causal, err, s);
+    case 128: return launch2<T, 128>(q, k, v, out, cu, sched, n_work, n_merge, kind, ws, H, H_kv, sl2, causal, err, s);
+    case 256: return launch2<T, 256>(q, k, v, out, cu, sched, n_work, n_merge, kind, ws, H, H_kv, sl2, causal, err, s);
   }
   return fail(MI_ERR_UNSUPPORTED,
               "mi_varlen_prefill: head_dim %d is not supported by the HIP prefill kernel "
@@ -1847,6 +2483,181 @@ int duo_schedule(const int32_t* cu, const std::vector<Piece>& pieces, const std:
   return words;
 }
 
+// Tall kernel schedule: {n_workgroups, n_counters, n_partials, layout}, n_workgroups entries
+// of Tall::ENTRY_WORDS {first item word, item count, the first item's six words}, then the
+// items, Tall::ITEM_WORDS words each (see the kernel). 128-row query tiles of every segment
+// count their 64-key steps; a tile x head whose steps exceed a cap C is cut into
+// ceil(steps / C) key ranges of near-equal length, the last one (it holds the diagonal) the
+// owner. Items are dealt longest-first to the least-loaded workgroup (LPT), the items of a
+// KV head on the workgroups of its XCD (or block of XCDs) when the launch fills the chip, so
+// its K and V stay in that L2. An item costs its steps plus kItemCost (its start and end), an
+// owner kMergeCost more per producer; C is the cap, tried from kMinCap up to the longest
+// tile, whose deal has the smallest most-loaded workgroup (ties: the larger cap, fewer
+// pieces). Each workgroup's list then runs its producer pieces first, so no owner waits on a
+// piece queued behind another owner.
+#ifndef MIATTN_TALL_CAP
+#define MIATTN_TALL_CAP 0  // > 0: a fixed piece cap in key steps instead of the search
+#endif
+#ifndef MIATTN_TALL_ITEM_COST
+#define MIATTN_TALL_ITEM_COST 3
+#endif
+#ifndef MIATTN_TALL_MERGE_COST
+#define MIATTN_TALL_MERGE_COST 2
+#endif
+int tall_schedule(const int32_t* cu, int n_seqs, int H, int H_kv, int D, int causal, int32_t* out, int capacity,
+                  int* n_split_tiles = nullptr) {
+  using W = Tall<128>;
+  constexpr int kCUs = 256, kMinCap = 4, kMaxPieces = 32;
+  constexpr int kItemCost = MIATTN_TALL_ITEM_COST, kMergeCost = MIATTN_TALL_MERGE_COST;
+  const int slots = kCUs * W::PER_CU;
+  struct TTile { int seq, tile, steps; };
+  std::vector<TTile> tiles;
+  int max_steps = 0;
+  for (int s = 0; s < n_seqs; ++s) {
+    const int L = cu[s + 1] - cu[s];
+    const int n = (L + W::BQ - 1) / W::BQ;
+    for (int t = 0; t < n; ++t) {
+      const int end = std::min(L, (t + 1) * W::BQ);
+      const int steps = causal ? (end + W::BK - 1) / W::BK : (L + W::BK - 1) / W::BK;
+      tiles.push_back({s, t, steps});
+      max_steps = std::max(max_steps, steps);
+    }
+  }
+  if (max_steps > 65535) return fail(MI_ERR_UNSUPPORTED, "mi_varlen_schedule: segment too long for the tall kernel");
+  if (H > 65535) return fail(MI_ERR_UNSUPPORTED, "mi_varlen_schedule: the tall kernel takes at most 65535 heads");
+  struct TPiece { int tile, t0, t1, role, n_prod, cost; };
+  const int G = H / H_kv;
+  std::vector<TPiece> pieces;
+  std::vector<std::vector<int>> lists;
+  int n_wg = 0;
+  auto cut = [&](int cap) {
+    pieces.clear();
+    for (int i = 0; i < int(tiles.size()); ++i) {
+      const int S = tiles[i].steps;
+      const int n = S > cap ? std::min(kMaxPieces, (S + cap - 1) / cap) : 1;
+      for (int p = 0; p < n; ++p) {
+        const int t0 = int(int64_t(p) * S / n), t1 = int(int64_t(p + 1) * S / n);
+        const int role = n == 1 ? W::ROLE_WHOLE : p + 1 < n ? W::ROLE_PRODUCER : W::ROLE_OWNER;
+        const int cost = (t1 - t0) + kItemCost + (role == W::ROLE_OWNER ? kMergeCost * (n - 1) : 0);
+        pieces.push_back({i, t0, t1, role, n - 1, cost});
+      }
+    }
+  };
+  // deal (piece, head) items; returns the most-loaded workgroup's cost
+  auto deal = [&]() -> int64_t {
+    const int64_t n_items = int64_t(pieces.size()) * H;
+    n_wg = int(std::min<int64_t>(slots, n_items));
+    const bool full = n_wg == slots;
+    const int n_groups = !full ? 1 : H_kv % kXcds == 0 ? kXcds : kXcds % H_kv == 0 ? H_kv : 1;
+    const int xcds_per_group = kXcds / n_groups;
+    std::vector<int> order(pieces.size());
+    for (int i = 0; i < int(order.size()); ++i) order[i] = i;
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return pieces[a].cost > pieces[b].cost; });
+    lists.assign(n_wg, {});
+    int64_t worst = 0;
+    for (int grp = 0; grp < n_groups; ++grp) {
+      std::vector<std::pair<int64_t, int>> heap;
+      for (int w = 0; w < n_wg; ++w) {
+        if ((w % kXcds) / xcds_per_group == grp) heap.push_back({0, w});
+      }
+      auto cmp = [](const std::pair<int64_t, int>& a, const std::pair<int64_t, int>& b) { return a > b; };
+      std::make_heap(heap.begin(), heap.end(), cmp);
+      for (int p : order) {
+        for (int h = 0; h < H; ++h) {
+          if ((h / G) % n_groups != grp) continue;
+          std::pop_heap(heap.begin(), heap.end(), cmp);
+          auto& top = heap.back();
+          lists[top.second].push_back(p * H + h);
+          top.first += pieces[p].cost;
+          worst = std::max(worst, top.first);
+          std::push_heap(heap.begin(), heap.end(), cmp);
+        }
+      }
+    }
+    return worst;
+  };
+  int best_cap = max_steps;
+  int64_t best = INT64_MAX;
+  for (int cap = MIATTN_TALL_CAP > 0 ? std::min(MIATTN_TALL_CAP, max_steps) : std::min(kMinCap, max_steps);
+       cap <= (MIATTN_TALL_CAP > 0 ? std::min(MIATTN_TALL_CAP, max_steps) : max_steps); ++cap) {
+    cut(cap);
+    const int64_t worst = deal();
+    if (worst <= best) {
+      best = worst;
+      best_cap = cap;
+    }
+  }
+  cut(best_cap);
+  deal();
+  // producers first in every list (stable), so a producer never waits behind an owner
+  for (auto& lst : lists) {
+    std::stable_partition(lst.begin(), lst.end(),
+                          [&](int id) { return pieces[id / H].role == W::ROLE_PRODUCER; });
+  }
+  // counters (one per split tile x head) and partial slots (one per producer piece x head,
+  // a tile's producers contiguous for each head)
+  std::vector<int> tile_counter(tiles.size(), -1), tile_slot(tiles.size(), -1);
+  int n_counters = 0, n_partials = 0;
+  for (const TPiece& pc : pieces) {
+    if (pc.role == W::ROLE_OWNER && tile_counter[pc.tile] < 0) {
+      tile_counter[pc.tile] = n_counters;
+      n_counters += H;
+      tile_slot[pc.tile] = n_partials;
+      n_partials += pc.n_prod * H;
+    }
+  }
+  if (n_counters >= (1 << 24)) return fail(MI_ERR_UNSUPPORTED, "mi_varlen_schedule: too many split tiles");
+  if (n_split_tiles != nullptr) *n_split_tiles = n_counters;
+  constexpr int EW = W::ENTRY_WORDS, IW = W::ITEM_WORDS;
+  const int64_t n_items = int64_t(pieces.size()) * H;
+  const int64_t words64 = kSchedHeader + EW * int64_t(n_wg) + IW * n_items;
+  if (words64 > INT32_MAX) return fail(MI_ERR_UNSUPPORTED, "mi_varlen_schedule: schedule too large");
+  const int words = int(words64);
+  if (out == nullptr) return words;
+  if (capacity < words) return fail(MI_ERR_INVALID, "mi_varlen_schedule: capacity %d < %d words", capacity, words);
+  out[0] = n_wg;
+  out[1] = n_counters;
+  out[2] = n_partials;
+  out[3] = layout_word(kTall, D, W::BQ);
+  int32_t* table = out + kSchedHeader;
+  int item_word = kSchedHeader + EW * n_wg;
+  int32_t* iw = out + item_word;
+  for (int w = 0; w < n_wg; ++w) {
+    int32_t* e = table + EW * w;
+    std::fill(e, e + EW, 0);
+    e[0] = item_word;
+    e[1] = int(lists[w].size());
+    for (size_t i = 0; i < lists[w].size(); ++i) {
+      const int id = lists[w][i];
+      const TPiece& pc = pieces[id / H];
+      const int h = id % H;
+      const TTile& tl = tiles[pc.tile];
+      // a producer's slot: its tile's first slot for this head plus its index among the
+      // tile's producers (pieces of a tile are consecutive, producers first)
+      int slot = 0, counter = 0;
+      if (pc.role != W::ROLE_WHOLE) {
+        counter = tile_counter[pc.tile] + h;
+        const int base = tile_slot[pc.tile] + h * pc.n_prod;
+        int index = 0;
+        if (pc.role == W::ROLE_PRODUCER) {
+          for (int j = id / H - 1; j >= 0 && pieces[j].tile == pc.tile; --j) ++index;
+        }
+        slot = base + index;
+      }
+      iw[0] = cu[tl.seq];
+      iw[1] = cu[tl.seq + 1] - cu[tl.seq];
+      iw[2] = int((uint32_t(tl.tile) << 16) | uint32_t(h));
+      iw[3] = int((uint32_t(pc.t0) << 16) | uint32_t(pc.t1));
+      iw[4] = int((uint32_t(pc.role) << 30) | (uint32_t(pc.n_prod) << 24) | uint32_t(counter));
+      iw[5] = slot;
+      if (i == 0) std::copy(iw, iw + IW, e + 2);
+      iw += IW;
+      item_word += IW;
+    }
+  }
+  return words;
+}
+
 size_t partial_bytes(int n_partials, int H, int D, int rows) {
   return size_t(n_partials) * H * rows * (D + 2) * sizeof(float);
 }
@@ -1858,8 +2669,11 @@ extern "C" int mi_varlen_schedule_for(const int32_t* host_cu_seqlens, int n_seqs
                                       int D, int causal, int kernel, int32_t* host_schedule,
                                       int capacity) {
   using namespace miattn;
-  if (kernel < MI_PREFILL_AUTO || kernel > MI_PREFILL_DUO || kernel == 2) {
+  if (kernel < MI_PREFILL_AUTO || kernel > MI_PREFILL_TALL || kernel == 2) {
     return fail(MI_ERR_INVALID, "mi_varlen_schedule: unknown prefill kernel %d", kernel);
+  }
+  if (kernel == MI_PREFILL_TALL && D != 64 && D != 128) {
+    return fail(MI_ERR_UNSUPPORTED, "mi_varlen_schedule: the tall kernel takes head_dim 64 or 128, got %d", D);
   }
   if (kernel == MI_PREFILL_RING && D != 64 && D != 128) {
     return fail(MI_ERR_UNSUPPORTED, "mi_varlen_schedule: the ring kernel takes head_dim 64 or 128, got %d", D);
@@ -1885,10 +2699,27 @@ extern "C" int mi_varlen_schedule_for(const int32_t* host_cu_seqlens, int n_seqs
   // ring kernel (64, 128) or the register-staged kernel (256). The caller may name a kernel
   // instead.
   const bool duo_heads = H <= 255;
+  for (int s = 0; s < n_seqs; ++s) {
+    if (host_cu_seqlens[s + 1] - host_cu_seqlens[s] <= 0) {
+      return fail(MI_ERR_INVALID, "mi_varlen_schedule: segment %d is empty", s);
+    }
+  }
+  // by default head_dim 64/128 batches with a segment of kTallMinLen tokens or more run the
+  // tall kernel when its schedule needs no split pieces
+  bool tall_default = false;
+  if (kernel == MI_PREFILL_AUTO && (D == 64 || D == 128) && max_len >= kTallMinLen && H <= 65535) {
+    int n_split = -1;
+    if (tall_schedule(host_cu_seqlens, n_seqs, H, H_kv, D, causal, nullptr, 0, &n_split) > 0 && n_split == 0) {
+      tall_default = true;
+    }
+  }
   const int kind = kernel == MI_PREFILL_STAGED ? kStaged : kernel == MI_PREFILL_RING ? kRing
-                 : kernel == MI_PREFILL_DUO ? kDuo
+                 : kernel == MI_PREFILL_DUO ? kDuo : kernel == MI_PREFILL_TALL || tall_default ? kTall
                  : (D == 64 || D == 128) ? (max_len >= kRingMinLen || !duo_heads ? kRing : kDuo)
                  : D == 256 && duo_heads ? kDuo : kStaged;
+  if (kind == kTall) {
+    return tall_schedule(host_cu_seqlens, n_seqs, H, H_kv, D, causal, host_schedule, capacity);
+  }
   const bool ring = kind != kStaged;  // one workgroup per CU, split-K capable
   const int RW = kind_rows(kind);
   const int BN = kind_keys(kind);
@@ -1965,7 +2796,16 @@ extern "C" int mi_varlen_schedule(const int32_t* host_cu_seqlens, int n_seqs, in
 extern "C" size_t mi_varlen_workspace_size(const int32_t* host_schedule, int H) {
   using namespace miattn;
   if (host_schedule == nullptr || H < 1) return 0;
+  if (layout_kind(host_schedule[3]) == kTall) {
+    return tall_workspace_bytes(host_schedule[1], host_schedule[2], layout_d(host_schedule[3]));
+  }
   return partial_bytes(host_schedule[2], H, layout_d(host_schedule[3]), layout_rows(host_schedule[3]));
+}
+
+extern "C" int mi_prefill_wait_limit(int polls) {
+  const int previous = miattn::g_wait_limit;
+  if (polls >= 0) miattn::g_wait_limit = polls;
+  return previous;
 }
 
 extern "C" int mi_varlen_prefill(const void* q, const void* k, const void* v, void* out,
@@ -1973,7 +2813,7 @@ extern "C" int mi_varlen_prefill(const void* q, const void* k, const void* v, vo
                                  int max_seqlen, const int32_t* schedule, int n_work, int n_merge,
                                  int n_partials, int layout, int H, int H_kv, int D, float scale,
                                  int causal, int dtype, void* workspace, size_t workspace_bytes,
-                                 void* stream) {
+                                 int32_t* error_word, void* stream) {
   using namespace miattn;
   if (dtype != MI_BF16 && dtype != MI_F16) {
     return fail(MI_ERR_UNSUPPORTED,
@@ -1995,15 +2835,15 @@ extern "C" int mi_varlen_prefill(const void* q, const void* k, const void* v, vo
   }
   const int rows = layout_rows(layout);
   const int kind = layout_kind(layout);
-  const bool split_capable = kind == kRing || kind == kDuo;
-  if (layout_d(layout) != D || kind < kStaged || kind > kDuo || kind == 2 || rows != kind_rows(kind) ||
+  const bool split_capable = kind == kRing || kind == kDuo || kind == kTall;
+  if (layout_d(layout) != D || kind < kStaged || kind > kTall || kind == 2 || rows != kind_rows(kind) ||
       (kind == kRing && D != 64 && D != 128) || (kind == kDuo && D != 64 && D != 128 && D != 256) ||
-      (n_merge > 0) != (n_partials > 0) ||
+      (kind == kTall && D != 64 && D != 128) || (n_merge > 0) != (n_partials > 0) ||
       (n_merge > 0 && !split_capable)) {
     return fail(MI_ERR_INVALID, "mi_varlen_prefill: schedule (layout 0x%x) does not match head_dim %d",
                 layout, D);
   }
-  const size_t need = partial_bytes(n_partials, H, D, rows);
+  const size_t need = kind == kTall ? tall_workspace_bytes(n_merge, n_partials, D) : partial_bytes(n_partials, H, D, rows);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
     return fail(MI_ERR_WORKSPACE, "mi_varlen_prefill: workspace of %zu bytes needed, got %zu", need,
                 workspace == nullptr ? size_t(0) : workspace_bytes);
@@ -2012,13 +2852,15 @@ extern "C" int mi_varlen_prefill(const void* q, const void* k, const void* v, vo
   if (!al(q) || !al(k) || !al(v) || !al(out) || (need > 0 && !al(workspace))) {
     return fail(MI_ERR_UNSUPPORTED, "mi_varlen_prefill: q/k/v/out/workspace must be 16-byte aligned");
   }
+  if (error_word != nullptr && reinterpret_cast<uintptr_t>(error_word) % 4 != 0) {
+    return fail(MI_ERR_INVALID, "mi_varlen_prefill: error_word must be 4-byte aligned");
+  }
   const float sl2 = float(double(scale) * 1.4426950408889634);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  float* partials = static_cast<float*>(workspace);
   if (dtype == MI_BF16) {
-    return launch1<bf16_t>(D, q, k, v, out, cu_seqlens, schedule, n_work, n_merge, kind, partials, H,
-                           H_kv, sl2, causal, s);
+    return launch1<bf16_t>(D, q, k, v, out, cu_seqlens, schedule, n_work, n_merge, kind, workspace, H,
+                           H_kv, sl2, causal, error_word, s);
   }
-  return launch1<f16_t>(D, q, k, v, out, cu_seqlens, schedule, n_work, n_merge, kind, partials, H,
-                        H_kv, sl2, causal, s);
+  return launch1<f16_t>(D, q, k, v, out, cu_seqlens, schedule, n_work, n_merge, kind, workspace, H,
+                        H_kv, sl2, causal, error_word, s);
 }

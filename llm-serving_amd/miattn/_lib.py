@@ -122,11 +122,12 @@ SIGNATURES: dict[str, tuple] = {
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
          _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_int,
-         _c_int, _c_void_p, _c_size_t, _c_void_p],
+         _c_int, _c_void_p, _c_size_t, _c_void_p, _c_void_p],
     ),
+    "mi_prefill_wait_limit": (_c_int, [_c_int]),
 }
 
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 
 def _load():

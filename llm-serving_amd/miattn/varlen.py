@@ -38,7 +38,7 @@ import torch.nn.functional as F
 from . import _lib
 from ._contract import Rule, as_index, enforce
 
-__all__ = ["HipVarlen", "SdpaVarlen", "backend_for", "segment_bounds", "validate_packed"]
+__all__ = ["HipVarlen", "SdpaVarlen", "backend_for", "check_prefill_errors", "segment_bounds", "validate_packed"]
 
 
 def _entries(cu_seqlens) -> list:
@@ -166,6 +166,9 @@ class _Schedules:
 
     @staticmethod
     def _build(bounds, H, H_kv, D, causal, device, kernel):
+        # the workspace lives with the schedule: the tall kernel's split-item counters at
+        # its head must be zero before the first launch (every launch leaves them zero), so
+        # it is zeroed once here and reused by every call of this packed group
         n_seqs = len(bounds) - 1
         host_cu = (ctypes.c_int32 * len(bounds))(*bounds)
         n_words = _lib.lib.mi_varlen_schedule_for(host_cu, n_seqs, H, H_kv, D, int(causal), kernel, None, 0)
@@ -181,10 +184,49 @@ class _Schedules:
             sched=torch.frombuffer(bytearray(words), dtype=torch.int32).to(device),
             header=tuple(int(words[i]) for i in range(4)),
             ws_bytes=ws_bytes,
+            ws=torch.zeros(ws_bytes, dtype=torch.uint8, device=device) if ws_bytes else None,
         )
 
 
 _SCHEDULES = _Schedules()
+
+#: what the kernels' error word codes mean (csrc/varlen_prefill.hip, kErr*)
+_ERROR_CODES = {
+    1: "a tall-kernel owner piece gave up waiting for its producer pieces",
+    2: "a head_dim 256 duo wave gave up waiting for its partner wave",
+}
+_ERROR_WORDS: dict = {}
+
+
+def _device_key(device) -> torch.device:
+    dev = torch.device(device) if device is not None else torch.device("cuda")
+    return torch.device(dev.type, dev.index if dev.index is not None else torch.cuda.current_device())
+
+
+def _error_word(device) -> torch.Tensor:
+    """The device's prefill error word (one int32, zero when no launch has given up),
+    allocated once per device and kept for the life of the process, so a launch recorded in
+    a HIP graph keeps a valid address."""
+    key = _device_key(device)
+    word = _ERROR_WORDS.get(key)
+    if word is None:
+        word = _ERROR_WORDS[key] = torch.zeros(1, dtype=torch.int32, device=key)
+    return word
+
+
+def check_prefill_errors(device=None) -> None:
+    """Raise ``RuntimeError`` if a prefill launch on ``device`` (default: the current HIP
+    device) gave up one of its bounded waits since the last check; the output of that launch
+    is not to be trusted. One host read; the word is cleared when it raises."""
+    key = _device_key(device)
+    word = _ERROR_WORDS.get(key)
+    if word is None:
+        return
+    code = int(word.item())
+    if code:
+        word.zero_()
+        raise RuntimeError(f"prefill_varlen on {key}: {_ERROR_CODES.get(code, f'error code {code}')}; "
+                           "the output of that launch is not valid")
 
 
 class HipVarlen:
@@ -194,14 +236,18 @@ class HipVarlen:
     name = "hip-mfma-varlen"
 
     #: ``HipVarlen(kernel=...)`` names; ``None`` lets the library choose per batch
-    KERNELS = {None: -1, "staged": 0, "ring": 1, "duo": 3}
+    KERNELS = {None: -1, "staged": 0, "ring": 1, "duo": 3, "tall": 4}
 
-    def __init__(self, kernel: str | None = None) -> None:
+    def __init__(self, kernel: str | None = None, *, strict: bool = False) -> None:
+        """``strict=True`` checks the device error word after every call made outside HIP
+        graph capture (one host read per call, :func:`check_prefill_errors`); by default calls
+        never synchronise and the caller checks when it chooses."""
         _lib.require_library("the hip-mfma-varlen prefill backend")
         if kernel not in self.KERNELS:
             raise ValueError(f"unknown prefill kernel {kernel!r}; choose one of "
                              f"{sorted(k for k in self.KERNELS if k)}")
         self._kernel = self.KERNELS[kernel]
+        self._strict = bool(strict)
 
     def prefill_varlen(self, q, k, v, *, cu_seqlens: Sequence[int] | torch.Tensor, max_seqlen: int,
                        softmax_scale: float | None = None, causal: bool = True):
@@ -218,14 +264,15 @@ class HipVarlen:
         H_kv = int(k.shape[1])
         plan = _SCHEDULES.get(bounds, H, H_kv, D, causal, q.device, self._kernel)
         out = torch.empty_like(q)
-        ws = torch.empty(plan.ws_bytes, dtype=torch.uint8, device=q.device) if plan.ws_bytes else None
         rc = _lib.lib.mi_varlen_prefill(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), plan.cu.data_ptr(), len(bounds) - 1, total,
             int(max_seqlen), plan.sched.data_ptr(), *plan.header, H, H_kv, D, scale, int(bool(causal)),
-            _lib.dtype_code(q.dtype), None if ws is None else ws.data_ptr(), plan.ws_bytes,
-            _lib.current_stream(q.device),
+            _lib.dtype_code(q.dtype), None if plan.ws is None else plan.ws.data_ptr(), plan.ws_bytes,
+            _error_word(q.device).data_ptr(), _lib.current_stream(q.device),
         )
         _lib.check(rc, "prefill_varlen")
+        if self._strict and not torch.cuda.is_current_stream_capturing():
+            check_prefill_errors(q.device)
         return out
 
 
