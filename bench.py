@@ -235,7 +235,8 @@ def bench_prefill(stream, steps: int = 20, eager: bool = False):
         "prefill_us_per_layer": prefill_ms * 1e3,
         "prefill_tflops": tflops,
         "prefill_frac_mfma_peak": tflops / BF16_MFMA_PEAK_TFLOPS,
-        "prefill_tokens_per_s": sum(inp.lengths) / (prefill_ms * 1e-3),
+        # tokens through one forward's attention (28 layer calls), not one layer call
+        "prefill_attention_tokens_per_s_per_forward": sum(inp.lengths) / (N_LAYER * prefill_ms * 1e-3),
         "flop_per_layer": flop,
         "slot_write_us_per_layer": write_ms * 1e3,
         "slot_write_gbs": write_bytes / (write_ms * 1e-3) / 1e9,

@@ -100,8 +100,9 @@ int mi_kv_slot_write(const void* k, const void* v, const void* slot_ids, int slo
  * to the activation dtype (see csrc/decode_epilogue.hip). slot_ids as for mi_kv_slot_write (int32 or
  * int64 per slot_bits; pools (n_slots, H_kv, D) contiguous). A row with slot -1 has nothing to
  * write this step and is skipped silently; any other row whose position is outside
- * [0, n_pos) or whose slot is outside [0, n_slots) is not written and 1 + its index goes to
- * *error_word (may be NULL). D = 64, 128 or 256. qkv_parts = 0: qkv holds `dtype` values;
+ * [0, n_pos) or whose slot is outside [0, n_slots) is not written to the pools and 1 + its
+ * index goes to *error_word (may be NULL). Both kinds of row get zeros in q_out (and in
+ * k_out / v_out when given). D = 64, 128 or 256. qkv_parts = 0: qkv holds `dtype` values;
  * qkv_parts = n >= 1: qkv holds fp32 split-K partial sums [n][B][row_stride] (mi_rows_gemm
  * with n_split = n), summed in split order and rounded once to `dtype` before the above.
  * k_out / v_out (may be NULL): the roped k and the v rows also written packed, (B, H_kv, D)

@@ -68,13 +68,26 @@ __global__ __launch_bounds__(256) void qk_norm_rope_write_kernel(
   if (head >= n_heads || b >= B) return;  // wave-uniform
   // slot -1 marks a row with nothing to write this step (an idle or refused seat of a decode
   // step): skipped silently. Any other row whose position is outside the RoPE table or whose
-  // slot is outside the pool is not written at all and is reported (row + 1) through the
-  // error word.
+  // slot is outside the pool is not written to the pool and is reported (row + 1) through
+  // the error word. Either way the row's packed outputs (q_out, and k_out / v_out when given)
+  // are zero-filled, so a consumer that reads every row reads defined values.
   const int64_t pb = pos[b];
   const IdxT slot = slots[b];
-  if (slot == IdxT(-1)) return;
-  if (pb < 0 || pb >= n_pos || !(slot >= 0 && int64_t(slot) < n_slots)) {
-    if (lane == 0 && head == 0 && err != nullptr) atomicCAS(err, 0, b + 1);
+  const bool idle = slot == IdxT(-1);
+  if (idle || pb < 0 || pb >= n_pos || !(slot >= 0 && int64_t(slot) < n_slots)) {
+    if (!idle && lane == 0 && head == 0 && err != nullptr) atomicCAS(err, 0, b + 1);
+    T* row = nullptr;
+    if (head < H) {
+      row = q_out + (int64_t(b) * H + head) * D;
+    } else if (head < H + H_kv) {
+      if (k_out != nullptr) row = k_out + (int64_t(b) * H_kv + (head - H)) * D;
+    } else if (v_out != nullptr) {
+      row = v_out + (int64_t(b) * H_kv + (head - H - H_kv)) * D;
+    }
+    if (row != nullptr) {
+#pragma unroll
+      for (int j = 0; j < NE; ++j) row[lane + 64 * j] = from_f32<T>(0.0f);
+    }
     return;
   }
   const int64_t src = int64_t(b) * row_stride + int64_t(head) * D;

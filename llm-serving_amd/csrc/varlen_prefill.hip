@@ -93,21 +93,6 @@ __device__ __forceinline__ floatx16 mfma32(const uint4& a, const uint4& b, const
 
 // Two fp32 values -> one word of two 16-bit values, round to nearest even; one
 // v_cvt_pk_bf16_f32 on gfx950 for bf16.
-// acc + lo + hi of one packed word of two 16-bit values, in one v_dot2 against (1, 1):
-// the row sum of the probabilities as rounded for the PV MFMA.
-template <typename T>
-__device__ __forceinline__ float sum_pair(uint32_t w, float acc) {
-  if constexpr (std::is_same<T, bf16_t>::value) {
-    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w),
-                                           __builtin_bit_cast(bf16x2_t, 0x3F803F80u), acc, false);
-  } else {
-    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, w), __builtin_bit_cast(f16x2_t, 0x3C003C00u),
-                                  acc, false);
-  }
-}
-
 template <typename T>
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
   if constexpr (std::is_same<T, bf16_t>::value) {
@@ -777,17 +762,14 @@ __global__ __launch_bounds__(Ring<D>::THREADS, 1) void varlen_prefill_ring_kerne
       m_i[j] = m_new;
 #pragma unroll
       for (int e = 0; e < 16; ++e) sc[e] = fast_exp2(fmaf(sc[e], scale_log2, -m_use));
-      // the row sum from the packed P, as in the duo kernel (8192 tokens: 309.9 against
-      // 313.9 us)
+      // the row sum from the fp32 probabilities, as in the duo kernel
       float ls = l_i[j] * alpha[j];
 #pragma unroll
       for (int t2 = 0; t2 < 2; ++t2) {
         pB[j][t2] = make_uint4(pack2<T>(sc[8 * t2 + 0], sc[8 * t2 + 1]), pack2<T>(sc[8 * t2 + 2], sc[8 * t2 + 3]),
                                pack2<T>(sc[8 * t2 + 4], sc[8 * t2 + 5]), pack2<T>(sc[8 * t2 + 6], sc[8 * t2 + 7]));
-        ls = sum_pair<T>(pB[j][t2].x, ls);
-        ls = sum_pair<T>(pB[j][t2].y, ls);
-        ls = sum_pair<T>(pB[j][t2].z, ls);
-        ls = sum_pair<T>(pB[j][t2].w, ls);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ls += sc[8 * t2 + e];
       }
       l_i[j] = ls;
     }
@@ -1389,9 +1371,18 @@ __global__ __launch_bounds__(Duo<D>::THREADS, Duo<D>::PER_CU) void varlen_prefil
       m_i = m_new;
 #pragma unroll
       for (int e = 0; e < 16; ++e) sc[e] = fast_exp2(fmaf(sc[e], scale_log2, -m_use));
-      // P(t) packed here, in the block of this step's MFMAs, and pinned: left alone the
-      // compiler sinks the exponentials past the end of the step, beside the PV MFMAs that
-      // read P, where nothing hides them (2-3% of the kernel)
+      // The row sum is taken from the fp32 probabilities, before their rounding for the PV
+      // MFMA, as flash attention does. Summing the rounded ones (8 dot2) instead lowered the
+      // end-to-end greedy agreement with the CPU seat path (closed case 252 against 254 of
+      // 260 steps exact, trace case 1142 against 1153 of 1168), all fp32 near-ties.
+      float lsum = l_i * alpha;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) lsum += sc[e];
+      // P(t) packed here, in the block of this step's MFMAs, and pinned with the row sum:
+      // left alone the compiler sinks the exponentials past the end of the step, beside the
+      // PV MFMAs that read P, where nothing hides them (2-3% of the kernel), and keeps the
+      // fp32 probabilities live across the step's MFMAs for the sum (head_dim 256: 50.4
+      // against 38.2 us)
       uint4 pN[2];
 #pragma unroll
       for (int t2 = 0; t2 < 2; ++t2) {
@@ -1399,22 +1390,8 @@ __global__ __launch_bounds__(Duo<D>::THREADS, Duo<D>::PER_CU) void varlen_prefil
                             pack2<T>(sc[8 * t2 + 4], sc[8 * t2 + 5]), pack2<T>(sc[8 * t2 + 6], sc[8 * t2 + 7]));
       }
       asm volatile("" : "+v"(pN[0].x), "+v"(pN[0].y), "+v"(pN[0].z), "+v"(pN[0].w),
-                        "+v"(pN[1].x), "+v"(pN[1].y), "+v"(pN[1].z), "+v"(pN[1].w));
-      // the row sum is taken from the packed P, 8 dot2 in place of 16 adds, so that the
-      // fp32 probabilities die at the pack (summed from them, they stayed live across the
-      // step's MFMAs: 40.4 against 38.0 us at head_dim 256), and l sums the same rounded
-      // values that the PV MFMA weights V by
-      {
-        float ls = l_i * alpha;
-#pragma unroll
-        for (int t2 = 0; t2 < 2; ++t2) {
-          ls = sum_pair<T>(pN[t2].x, ls);
-          ls = sum_pair<T>(pN[t2].y, ls);
-          ls = sum_pair<T>(pN[t2].z, ls);
-          ls = sum_pair<T>(pN[t2].w, ls);
-        }
-        l_i = ls;
-      }
+                        "+v"(pN[1].x), "+v"(pN[1].y), "+v"(pN[1].z), "+v"(pN[1].w), "+v"(lsum));
+      l_i = lsum;
       floatx16 nxt = zero16();
       auto mfma_part = [&](int hf) {
 #pragma unroll
@@ -1908,11 +1885,11 @@ __global__ __launch_bounds__(Tall<D>::THREADS, Tall<D>::PER_CU) void varlen_pref
       issue(vseg, it, t, vb_free);
       if constexpr (kS) {
         if (t + 2 < it.t_end) issue(kseg, it, t + 2, kb_free);
-      } else {
-        if (more) {
-          issue(nkseg, nx, nx.t_first, kb0);
-          issue(nkseg, nx, nx.t_first + 1, kb1);
-        }
+      } else if (more) {
+        // issued after V(t), so the step's end waits for V(t) (the drain's) and leaves these
+        // in flight through the drain and the epilogue
+        issue(nkseg, nx, nx.t_first, kb0);
+        issue(nkseg, nx, nx.t_first + 1, kb1);
       }
       __builtin_amdgcn_s_setprio(1);
       fresh_bases();
@@ -2012,11 +1989,9 @@ __global__ __launch_bounds__(Tall<D>::THREADS, Tall<D>::PER_CU) void varlen_pref
                               pack2<T>(p8[6], p8[7]));
           // pinned here, in this group: left alone the compiler sinks the exponentials into
           // the next step, beside the PV MFMAs that read P
-          asm volatile("" : "+v"(pB[s4].x), "+v"(pB[s4].y), "+v"(pB[s4].z), "+v"(pB[s4].w));
-          ls = sum_pair<T>(pB[s4].x, ls);
-          ls = sum_pair<T>(pB[s4].y, ls);
-          ls = sum_pair<T>(pB[s4].z, ls);
-          ls = sum_pair<T>(pB[s4].w, ls);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) ls += p8[e];  // the row sum from the fp32 values, as in the duo kernel
+          asm volatile("" : "+v"(pB[s4].x), "+v"(pB[s4].y), "+v"(pB[s4].z), "+v"(pB[s4].w), "+v"(ls));
         }
         if constexpr (kS) {
           if (qg + 1 < NG) __builtin_amdgcn_sched_group_barrier(0x0100, PG, 0);
@@ -2041,7 +2016,11 @@ __global__ __launch_bounds__(Tall<D>::THREADS, Tall<D>::PER_CU) void varlen_pref
         for (int i = 0; i < DB; ++i) o[i] *= alpha;
       }
       __builtin_amdgcn_s_setprio(0);
-      wait_vm_lgkm0<0>();
+      if (!kS && more) {
+        wait_vm_lgkm0<2 * LPW>();
+      } else {
+        wait_vm_lgkm0<0>();
+      }
       bare_barrier();
     };
     auto drain = [&](const uint8_t* vb) {

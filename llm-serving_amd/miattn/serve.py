@@ -168,6 +168,13 @@ class SeatDecoder:
         self.tokens[seat] = first_token
         self.steps[seat] = 0
 
+    def force(self, seats: list[int], tokens: list[int]) -> None:
+        """Replace the named seats' next input tokens (teacher forcing); the picks already
+        recorded in the history stay as the step produced them."""
+        idx = torch.tensor(seats, dtype=torch.long)
+        self.tokens.index_put_((idx.to(self.tokens.device),),
+                               torch.tensor(tokens, dtype=torch.long).to(self.tokens.device))
+
     def retire(self, seat: int, n_tokens: int) -> list[int]:
         """The seat's decode tokens (one device read) and the seat made idle."""
         out = self.history[seat, :n_tokens].tolist()
@@ -238,7 +245,14 @@ class ContinuousServer:
         self.max_prefill_tokens = int(max_prefill_tokens)
         self.seats = SeatDecoder(model, self.pool, max_batch, self.blocks.blocks_for(max_prompt + max_new), max_new)
         self.stream = stream
+        self.n_blocks = int(n_blocks)
         self.steps_run = 0
+        # concurrency seen by the last run(): the most seats active in one decode step,
+        # admissions made while other requests were decoding, and retirements that left
+        # other requests decoding
+        self.max_active = 0
+        self.admitted_mid_decode = 0
+        self.retired_mid_decode = 0
 
     def warm(self) -> None:
         """Capture the step graph and run one throwaway prefill (GEMM algorithm choice,
@@ -249,24 +263,49 @@ class ContinuousServer:
         self.blocks.give_back(blocks)
         torch.cuda.synchronize()
 
-    def run(self, trace: list[TraceRequest], *, realtime: bool = True) -> tuple[list[RequestRecord], float]:
+    def run(self, trace: list[TraceRequest], *, realtime: bool = True, step_s: float | None = None,
+            forced: dict | None = None) -> tuple[list[RequestRecord], float]:
         """Serve ``trace``; returns the per-request records and the wall time.
 
         ``realtime=False`` replays the same schedule on a virtual clock: instead of
         sleeping until the next arrival when nothing is active, the clock jumps to it (the
-        GPU work and its timing are unchanged; tests use this)."""
-        if any(r.max_new > self.max_new or len(r.prompt) + r.max_new > self.seats.table.shape[1]
-               * self.blocks.block_size for r in trace):
-            raise ValueError("a request does not fit the server's prompt/budget bounds")
+        GPU work and its timing are unchanged; tests use this). ``step_s`` (virtual clock
+        only) makes the clock fully synthetic: each prefill group and each decode step
+        advances it by ``step_s`` seconds, so admissions and retirements follow the trace
+        deterministically, whatever the GPU's speed.
+
+        ``forced`` (request idx -> tokens, at least ``max_new`` of them) runs the requests
+        teacher-forced: every step's input token is the given one rather than the previous
+        pick, while each record still holds the picks the GPU made. A token-by-token
+        comparison against another implementation's greedy tokens then compares every
+        step on the same context, not just the prefix before a first divergence.
+
+        A request that could never be admitted -- more blocks than the whole pool, or past
+        the prompt / token budget the seats were sized for -- raises ``ValueError`` before
+        anything runs."""
+        if step_s is not None and (realtime or step_s <= 0):
+            raise ValueError("step_s needs realtime=False and a positive step")
+        for r in trace:
+            if r.max_new < 1 or r.max_new > self.max_new:
+                raise ValueError(f"request {r.idx}: max_new {r.max_new} outside [1, {self.max_new}]")
+            if len(r.prompt) + r.max_new > self.seats.table.shape[1] * self.blocks.block_size:
+                raise ValueError(f"request {r.idx}: {len(r.prompt)} + {r.max_new} tokens exceed a seat's "
+                                 f"{self.seats.table.shape[1] * self.blocks.block_size} positions")
+            if self.blocks.blocks_for(len(r.prompt) + r.max_new) > self.n_blocks:
+                raise ValueError(f"request {r.idx} needs {self.blocks.blocks_for(len(r.prompt) + r.max_new)} "
+                                 f"blocks; the pool has {self.n_blocks}")
+            if forced is not None and len(forced.get(r.idx, ())) < r.max_new:
+                raise ValueError(f"request {r.idx}: forced tokens must cover its {r.max_new} tokens")
         records = {r.idx: RequestRecord(r.idx, r.arrival_s, len(r.prompt)) for r in trace}
         queue = sorted(trace, key=lambda r: (r.arrival_s, r.idx))
         free_seats = list(range(self.max_batch - 1, -1, -1))
         active: dict[int, tuple[TraceRequest, list[int], int]] = {}  # seat -> (request, blocks, tokens so far)
-        skew = 0.0  # virtual-clock offset
+        skew = 0.0  # virtual-clock offset (the whole clock when step_s is given)
         t0 = time.perf_counter()
+        self.max_active = self.admitted_mid_decode = self.retired_mid_decode = 0
 
         def now() -> float:
-            return time.perf_counter() - t0 + skew
+            return skew if step_s is not None else time.perf_counter() - t0 + skew
 
         head = 0
         while head < len(queue) or active:
@@ -293,15 +332,19 @@ class ContinuousServer:
                 tokens += len(req.prompt)
                 head += 1
             if group:
+                if active:
+                    self.admitted_mid_decode += len(group)
                 t_admit = now()
                 logits = self.model.prefill([list(r.prompt) for r, _ in group], self.pool, [b for _, b in group])
                 first = logits.argmax(-1)
                 torch.cuda.synchronize()
+                if step_s is not None:
+                    skew += step_s
                 t_first = now()
                 first_host = first.tolist()
                 for (req, blocks), tok in zip(group, first_host):
                     seat = free_seats.pop()
-                    self.seats.admit(seat, blocks, len(req.prompt), tok)
+                    self.seats.admit(seat, blocks, len(req.prompt), tok if forced is None else forced[req.idx][0])
                     rec = records[req.idx]
                     rec.admitted_s, rec.first_token_s, rec.tokens = t_admit, t_first, [tok]
                     active[seat] = (req, blocks, 1)
@@ -310,17 +353,29 @@ class ContinuousServer:
             if not active:
                 continue
             # ---- one decode step of every seat
+            self.max_active = max(self.max_active, len(active))
             self.seats.step()
             torch.cuda.synchronize()
+            if step_s is not None:
+                skew += step_s
             t_step = now()
             self.steps_run += 1
+            force_seats, force_tokens = [], []
             for seat in list(active):
                 req, blocks, n = active[seat]
                 active[seat] = (req, blocks, n + 1)
                 if n + 1 == req.max_new:
                     self._finish(seat, active, free_seats, records, t_step)
+                    if active:
+                        self.retired_mid_decode += 1
+                elif forced is not None:
+                    force_seats.append(seat)
+                    force_tokens.append(forced[req.idx][n])
+            if force_seats:
+                self.seats.force(force_seats, force_tokens)
         self.seats.check()
-        return [records[r.idx] for r in trace], time.perf_counter() - t0 + skew
+        wall = skew if step_s is not None else time.perf_counter() - t0 + skew
+        return [records[r.idx] for r in trace], wall
 
     def _finish(self, seat, active, free_seats, records, t) -> None:
         req, blocks, n = active.pop(seat)

@@ -6,9 +6,13 @@ N(0, 0.02)):
 
 * ``closed``: 4 prompts of 37/64/100/128 uniform ids (torch.Generator seed 1), the prefill
   token and 64 decode steps each (65 greedy tokens per request);
-* ``trace``: a sized-down config 5 -- 8 requests of ``miattn.serve.poisson_trace`` (4 req/s,
-  prompts lognormal(median 256, sigma 0.6) clipped to [32, 2048], seed 5) with 32 new tokens
-  each instead of 128.
+* ``trace``: config 5 at its concurrency, time-compressed -- 16 requests of
+  ``miattn.serve.poisson_trace`` (prompts lognormal(median 256, sigma 0.6) clipped to
+  [32, 2048], seed 5) at 400 req/s instead of 4 (the arrivals x 1/100), with 128 new tokens
+  for every third request and 32 or 48 for the others. Served on the synthetic clock of
+  ``ContinuousServer.run(step_s=TRACE_STEP_S)``, one arrival lands about every decode step:
+  the requests are admitted in small groups while earlier ones decode, up to 16 seats
+  decode together, and the short requests retire while the long ones go on.
 
 The reference's gate is exact greedy agreement, with every miss first checked as a
 near-tie against an fp32 oracle (reference
@@ -17,7 +21,9 @@ records, besides the bf16 seat path's token (``tokens``): the same model in fp32
 RoPE tables and KV upcast) run teacher-forced on the bf16 path's tokens, its logits at the
 union of the bf16 top-8 and fp32 top-8 ids (``cand_ids``/``cand_fp32``), and ``bf16_err``,
 the largest |bf16 - fp32| logit difference over those ids -- how far the bf16 computation
-itself strays from fp32 at that step. Runs in well under a minute on 8 cores:
+itself strays from fp32 at that step. The closed case indexes these ``[step][row]``, the
+trace case ``[request][step]`` (its requests have different lengths). Runs in about two
+minutes on 8 cores:
 
     python tests/golden/make_greedy_gate.py
 """
@@ -38,6 +44,11 @@ from miattn.serve import poisson_trace  # noqa: E402
 from oracle.qwen3_seat import SeatQwen3  # noqa: E402
 
 SEED, TOP = 0, 8
+TRACE_N, TRACE_RATE, TRACE_SEED, TRACE_STEP_S = 16, 400.0, 5, 0.0025
+
+
+def trace_max_new(i: int) -> int:
+    return (128, 32, 48)[i % 3]
 
 
 def greedy(cfg, weights, prompts, steps, forced=None):
@@ -48,6 +59,21 @@ def greedy(cfg, weights, prompts, steps, forced=None):
     for s in range(steps):
         tok = out[-1].argmax(-1) if forced is None else torch.tensor([f[s] for f in forced])
         out.append(model.decode(tok).float())
+    return out
+
+
+def per_request(cfg, w16, w32, prompts, max_new) -> dict:
+    """The trace case: requests grouped by token budget, each group through :func:`case`,
+    the results re-indexed ``[request][step]``."""
+    out = {"lengths": [len(p) for p in prompts], "prompts": [list(p) for p in prompts], "tokens": [None] * len(prompts),
+           "cand_ids": [None] * len(prompts), "cand_fp32": [None] * len(prompts), "bf16_err": [None] * len(prompts)}
+    for budget in sorted(set(max_new)):
+        rows = [i for i, m in enumerate(max_new) if m == budget]
+        rec = case(cfg, w16, w32, [prompts[i] for i in rows], budget - 1)
+        for j, i in enumerate(rows):
+            out["tokens"][i] = rec["tokens"][j]
+            for key in ("cand_ids", "cand_fp32", "bf16_err"):
+                out[key][i] = [step[j] for step in rec[key]]
     return out
 
 
@@ -78,14 +104,16 @@ def main() -> None:
     w32 = {k: v.float() for k, v in w16.items()}
     gen = torch.Generator().manual_seed(1)
     closed = [torch.randint(0, cfg.vocab, (n,), generator=gen).tolist() for n in (37, 64, 100, 128)]
-    trace = poisson_trace(8, rate=4.0, vocab=cfg.vocab, max_new=32, seed=5)
+    trace = poisson_trace(TRACE_N, rate=TRACE_RATE, vocab=cfg.vocab, seed=TRACE_SEED)
+    max_new = [trace_max_new(i) for i in range(TRACE_N)]
     out = {
         "weights_seed": SEED,
         "closed": {"steps": 64, **case(cfg, w16, w32, closed, 64)},
-        "trace": {"rate": 4.0, "seed": 5, "max_new": 32, "arrivals": [r.arrival_s for r in trace],
-                  **case(cfg, w16, w32, [list(r.prompt) for r in trace], 31)},
-        "note": "per case: tokens[r][s] is the bf16 seat path's greedy token s of request r (s=0 from the "
-                "prefill); cand_ids/cand_fp32/bf16_err are indexed [s][r]",
+        "trace": {"rate": TRACE_RATE, "seed": TRACE_SEED, "step_s": TRACE_STEP_S, "max_new": max_new,
+                  "arrivals": [r.arrival_s for r in trace],
+                  **per_request(cfg, w16, w32, [list(r.prompt) for r in trace], max_new)},
+        "note": "tokens[r][s] is the bf16 seat path's greedy token s of request r (s=0 from the prefill); "
+                "cand_ids/cand_fp32/bf16_err are indexed [s][r] in the closed case and [r][s] in the trace case",
     }
     path = Path(__file__).with_name("greedy_gate_seed0.json")
     path.write_text(json.dumps(out, separators=(",", ":")))

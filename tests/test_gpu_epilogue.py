@@ -81,12 +81,35 @@ def test_epilogue_rejects_bad_rows_without_writing():
         pool.check_writes()
     written = (pool.keys[0].view(pool.n_slots, -1) != 0).any(1)
     assert written.sum().item() == 3 and not written[slots[[0, 1, 3]].cpu()].logical_not().any()
+    # the rejected row's q is zero-filled rather than left as whatever the allocation held
+    q = pool.write_qk_norm_rope(0, slots, qkv, qn, kn, cos, sin, pos, 1e-6)
+    with pytest.raises(IndexError):
+        pool.check_writes()
+    assert not q[2].any() and q[[0, 1, 3]].abs().amax(-1).gt(0).all()
     pos[1] = cos.shape[0]  # outside the RoPE table
     slots[2] = 5
     pool2 = PagedPool(1, 64, 16, H_kv, D, dtype=dtype, device="cuda", n_head=H)
     pool2.write_qk_norm_rope(0, slots, qkv, qn, kn, cos, sin, pos, 1e-6)
     with pytest.raises(IndexError):
         pool2.check_writes()
+
+
+def test_epilogue_idle_rows_write_nothing_and_get_zero_outputs():
+    """slot -1 (an idle seat): nothing reaches the pool, no error is reported, and the row's
+    q (and packed k / v when asked for) are zeros, not the allocation's old contents."""
+    H, H_kv, D, dtype = 16, 8, 128, torch.bfloat16
+    qkv, qn, kn, cos, sin, pos, slots = _case(4, H, H_kv, D, dtype, seed=5)
+    slots[1] = -1
+    pool = PagedPool(1, 64, 16, H_kv, D, dtype=dtype, device="cuda", n_head=H, strict_writes=True)
+    k_out = torch.full((4, H_kv, D), 7.0, dtype=dtype, device="cuda")
+    v_out = torch.full((4, H_kv, D), 7.0, dtype=dtype, device="cuda")
+    q = pool.write_qk_norm_rope(0, slots, qkv, qn, kn, cos, sin, pos, 1e-6, k_out=k_out, v_out=v_out)
+    torch.cuda.synchronize()
+    written = (pool.keys[0].view(pool.n_slots, -1) != 0).any(1)
+    assert written.sum().item() == 3
+    assert not q[1].any() and not k_out[1].any() and not v_out[1].any()
+    for b in (0, 2, 3):
+        assert q[b].abs().amax(-1).gt(0).all() and torch.equal(pool.values[0].view(-1, H_kv, D)[slots[b]], v_out[b])
 
 
 def test_epilogue_validates_shapes():
