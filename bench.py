@@ -11,8 +11,9 @@ Algorithmic bytes per layer = sum(seqlen) * 2 * H_kv * D * 2 B (K and V read onc
 head) + q and out (2 * B * H * D * 2 B) + seqlen + block table.
 
 Extra fields: packed prefill (config 3) TFLOP/s against bf16 MFMA peak, also at the
-Qwen3.5 attention shape (H 8 / H_kv 2 / head_dim 256), the packed KV slot write (config
-3) GB/s, long-context split-K decode (config 4), and the CPU baseline:
+Qwen3.5 attention shape (H 8 / H_kv 2 / head_dim 256) and for one 8192-token segment
+(``prefill_long``, the default kernel there), the packed KV slot write (config 3) GB/s,
+long-context split-K decode (config 4), and the CPU baseline:
 the reference's seat path (contiguous slab + baddbmm decode, bf16 softmax) timed on this
 host's cores on one layer of the same config-2 inputs, after checking the GPU output
 against it.
@@ -21,6 +22,7 @@ against it.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -428,6 +430,65 @@ def bench_prefill_qwen35(stream, steps: int = 20, eager: bool = False) -> dict:
     }
 
 
+def bench_prefill_long(stream, steps: int = 5, eager: bool = False, L: int = 8192) -> dict:
+    """One ``L``-token segment at the Qwen3 attention shape (H16/H_kv8/D128 bf16), the
+    library's default kernel (the tall kernel at this length): 28 layer calls per step,
+    HIP-graph replay. Checked before it is timed on sampled query rows (the last 64 and 64
+    spread over the segment, 4 heads) against an fp32 softmax of those rows over their
+    whole causal key range, which the CPU computes in a second (the whole segment's fp32
+    oracle would take minutes)."""
+    from miattn import HipVarlen, _lib
+    from miattn import workloads as W
+
+    inp = W.prefill_config3(device="cuda", lengths=[L])
+    backend = HipVarlen()
+    H, D = inp.q.shape[1], inp.q.shape[2]
+    G = H // inp.k.shape[1]
+    # the kernel the library's default schedule names (header word 3, bits 20 and up)
+    cu = (ctypes.c_int32 * 2)(0, L)
+    n_words = _lib.lib.mi_varlen_schedule_for(cu, 1, H, inp.k.shape[1], D, 1, -1, None, 0)
+    words = (ctypes.c_int32 * n_words)()
+    _lib.lib.mi_varlen_schedule_for(cu, 1, H, inp.k.shape[1], D, 1, -1, words, n_words)
+    kernel = {0: "staged", 1: "ring", 3: "duo", 4: "tall"}[words[3] >> 20]
+    flop = 4 * H * D * L * (L + 1) // 2
+    got = backend.prefill_varlen(inp.q, inp.k, inp.v, cu_seqlens=inp.cu_seqlens, max_seqlen=L).float().cpu()
+    qc, kc, vc = inp.q.float().cpu(), inp.k.float().cpu(), inp.v.float().cpu()
+    rows = sorted(set(range(L - 64, L)) | set(range(0, L, L // 64)))
+    diff = 0.0
+    for h in (0, 5, 10, 15):
+        s = qc[rows, h] @ kc[:, h // G].T / D ** 0.5
+        s = s.masked_fill(torch.arange(L)[None, :] > torch.tensor(rows)[:, None], float("-inf"))
+        ref = torch.softmax(s, -1) @ vc[:, h // G]
+        diff = max(diff, (got[rows, h] - ref).abs().max().item())
+    if not diff <= 2e-2:
+        raise SystemExit(f"long-segment prefill disagrees with the fp32 rows: max|delta|={diff}")
+
+    def prefill_step():
+        for _ in range(N_LAYER):
+            backend.prefill_varlen(inp.q, inp.k, inp.v, cu_seqlens=inp.cu_seqlens, max_seqlen=L)
+
+    if eager:
+        with torch.cuda.stream(stream):
+            prefill_step()
+            torch.cuda.synchronize()
+            with EventTimer(stream) as t:
+                prefill_step()
+            step_ms = t.ms()
+    else:
+        step_ms, _ = time_graph(prefill_step, stream, steps, 1)
+    us = step_ms / N_LAYER * 1e3
+    tflops = flop / (us * 1e-6) / 1e12
+    return {
+        "workload": f"one {L}-token segment, H16/H_kv8/D128 bf16, default kernel, 28 layer calls, HIP-graph replay",
+        "kernel": kernel,
+        "prefill_us_per_layer": us,
+        "prefill_tflops": tflops,
+        "prefill_frac_mfma_peak": tflops / BF16_MFMA_PEAK_TFLOPS,
+        "flop_per_layer": flop,
+        "checked": {"max_abs_diff_vs_fp32_rows": diff, "rows": len(rows), "heads": 4},
+    }
+
+
 def bench_block32(stream, steps: int = 50) -> dict:
     """Config 2 with 32-token blocks (the reference's other contract block size): the same
     lengths and the same bytes in 4096 blocks of 32 per layer, checked then timed like the
@@ -643,7 +704,8 @@ def main() -> int:
         return 0
     if args.prefill_only:
         print(json.dumps({"prefill": bench_prefill(stream, args.steps, eager=args.eager),
-                          "prefill_qwen35": bench_prefill_qwen35(stream, args.steps, eager=args.eager)}),
+                          "prefill_qwen35": bench_prefill_qwen35(stream, args.steps, eager=args.eager),
+                          "prefill_long": bench_prefill_long(stream, eager=args.eager)}),
               flush=True)
         return 0
     log("building config-2 inputs (28 layers, 8192 blocks each)")
@@ -696,6 +758,9 @@ def main() -> int:
             f"slot write {line['prefill']['slot_write_gbs']:.1f} GB/s")
         line["prefill_qwen35"] = bench_prefill_qwen35(stream)
         log(f"prefill (Qwen3.5 shape, D256): {line['prefill_qwen35']['prefill_tflops']:.1f} TFLOP/s")
+        line["prefill_long"] = bench_prefill_long(stream)
+        log(f"prefill (one 8192-token segment, {line['prefill_long']['kernel']} kernel): "
+            f"{line['prefill_long']['prefill_tflops']:.1f} TFLOP/s")
         log("end-to-end TPOT (config 5 shape, B=32 ctx 2048)")
         line["e2e"] = bench_tpot(stream)
         line["tpot_ms"] = round(line["e2e"]["tpot_ms"], 4)
