@@ -196,8 +196,11 @@ class PagedPool:
         ``model/qwen35.py:207-210``) followed by ``PagedKV.write``; the kernel rounds each
         step to the pool dtype as those ops do. A row whose position is outside the tables or
         whose slot is outside the pool is not written and is reported by
-        :meth:`check_writes`. ``k_out``/``v_out`` (contiguous ``(B, n_kv_head, head_dim)``)
-        also receive the roped k and the v rows packed, for a packed prefill group.
+        :meth:`check_writes`. Slot -1 marks an idle seat (the seat decoder's rows with nothing
+        to do this step): that row writes nothing and reports nothing. Both kinds of row come
+        back as zeros in q (and in ``k_out``/``v_out``). ``k_out``/``v_out`` (contiguous
+        ``(B, n_kv_head, head_dim)``) also receive the roped k and the v rows packed, for a
+        packed prefill group.
         """
         layer = self._layer(layer)
         H, H_kv, D = self.n_head, self.n_kv_head, self.head_dim
