@@ -13,7 +13,8 @@ head) + q and out (2 * B * H * D * 2 B) + seqlen + block table.
 Extra fields: packed prefill (config 3) TFLOP/s against bf16 MFMA peak, also at the
 Qwen3.5 attention shape (H 8 / H_kv 2 / head_dim 256) and for one 8192-token segment
 (``prefill_long``, the default kernel there), the packed KV slot write (config 3) GB/s,
-long-context split-K decode (config 4), and the CPU baseline:
+long-context split-K decode (config 4), decode at the Qwen3.5 shape on the config-2 lengths
+(``decode_qwen35``), and the CPU baseline:
 the reference's seat path (contiguous slab + baddbmm decode, bf16 softmax) timed on this
 host's cores on one layer of the same config-2 inputs, after checking the GPU output
 against it.
@@ -504,6 +505,21 @@ def bench_block32(stream, steps: int = 50) -> dict:
             "frac_hbm_peak": res["gbs"] / HBM_PEAK_GBS}
 
 
+def bench_decode_qwen35(stream, steps: int = 50) -> dict:
+    """Config 2's lengths at the Qwen3.5 attention shape (H 8 / H_kv 2 / head_dim 256,
+    block size 16, 8192 blocks per layer, 28 layers): checked then timed like the
+    headline leg."""
+    from miattn import workloads as W
+
+    inp = W.paged_decode_config(device="cuda", H=8, H_kv=2, D=256)
+    res = bench_decode(inp, steps, 5, stream)
+    res.pop("out0")
+    del inp
+    torch.cuda.empty_cache()
+    return {"workload": "config2 lengths at H8/H_kv2/D256 bf16 (Qwen3.5 attention), 28 layers, HIP-graph replay",
+            **res, "frac_hbm_peak": res["gbs"] / HBM_PEAK_GBS}
+
+
 def bench_head_major(stream, steps: int = 50) -> dict:
     """Config 2 with head-major pools: each layer's K and V stored as (n_blocks, H_kv, 16,
     128), so a block holds each KV head's 16 tokens contiguously, and passed as the
@@ -673,6 +689,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--decode-only", action="store_true", help="only the headline decode leg (for profiling)")
     ap.add_argument("--e2e-only", action="store_true", help="only the end-to-end TPOT leg")
+    ap.add_argument("--qwen35-decode-only", action="store_true",
+                    help="only the Qwen3.5-shape decode leg (for profiling)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the config-3 prefill and slot-write legs (for profiling)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -701,6 +719,9 @@ def main() -> int:
     stream = torch.cuda.Stream()
     if args.e2e_only:
         print(json.dumps({"e2e": bench_tpot(stream), "config5_trace": bench_config5(stream)}), flush=True)
+        return 0
+    if args.qwen35_decode_only:
+        print(json.dumps({"decode_qwen35": bench_decode_qwen35(stream)}), flush=True)
         return 0
     if args.prefill_only:
         print(json.dumps({"prefill": bench_prefill(stream, args.steps, eager=args.eager),
@@ -775,6 +796,8 @@ def main() -> int:
         log(f"bs32: {line['decode_block32']['us_per_layer']:.2f} us/layer")
         line["decode_head_major"] = bench_head_major(stream)
         log(f"head-major pools: {line['decode_head_major']['us_per_layer']:.2f} us/layer")
+        line["decode_qwen35"] = bench_decode_qwen35(stream)
+        log(f"decode (Qwen3.5 shape, D256): {line['decode_qwen35']['us_per_layer']:.2f} us/layer")
         log("long-context decode (config 4)")
         line["long_context"] = bench_long_context(stream)
         log(f"config4: {line['long_context']['gbs']:.1f} GB/s")
