@@ -688,7 +688,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--decode-only", action="store_true", help="only the headline decode leg (for profiling)")
-    ap.add_argument("--e2e-only", action="store_true", help="only the end-to-end TPOT leg")
+    ap.add_argument("--e2e-only", action="store_true", help="only the end-to-end legs (TPOT and the config-5 trace)")
+    ap.add_argument("--tpot-only", action="store_true", help="only the end-to-end TPOT leg (for profiling)")
     ap.add_argument("--qwen35-decode-only", action="store_true",
                     help="only the Qwen3.5-shape decode leg (for profiling)")
     ap.add_argument("--prefill-only", action="store_true",
@@ -719,6 +720,9 @@ def main() -> int:
     stream = torch.cuda.Stream()
     if args.e2e_only:
         print(json.dumps({"e2e": bench_tpot(stream), "config5_trace": bench_config5(stream)}), flush=True)
+        return 0
+    if args.tpot_only:
+        print(json.dumps({"e2e": bench_tpot(stream)}), flush=True)
         return 0
     if args.qwen35_decode_only:
         print(json.dumps({"decode_qwen35": bench_decode_qwen35(stream)}), flush=True)

@@ -221,6 +221,33 @@ int mi_paged_decode(const void* q, const void* k_cache, const void* v_cache,
                     const int64_t* strides, float scale, int dtype, void* workspace,
                     size_t workspace_bytes, void* stream);
 
+/* mi_paged_decode_fused -- one launch pair for a decode step's attention from the packed
+ * q/k/v projection: what mi_qk_norm_rope_write followed by mi_paged_decode computes
+ * (reference: q_norm / k_norm, apply_rotary_emb and PagedKV.write, model/layers.py:193-211
+ * and model/paged.py:503-520, then paged_decode, model/triton_decode.py:250-328), with the
+ * same result bit for bit and the same pool contents afterwards, minus the epilogue launch
+ * and q's round trip through memory. Each decode workgroup computes its row's q (per-head
+ * RMSNorm x / rms * w and whole-head NeoX RoPE at pos[b], each op rounded to the dtype as
+ * in mi_qk_norm_rope_write); the workgroup holding the row's new token computes that
+ * token's k and v, writes them to k_cache / v_cache at slot_ids[b] and reads them from
+ * registers, not from the pool. Contract: the new token is the row's last one, pos[b] =
+ * seqlen[b] - 1 (the decode step's layout). A row with slot -1 is idle (nothing written;
+ * it should have seqlen 0). Any other row whose pos is outside [0, n_pos) or not seqlen - 1,
+ * or whose slot is outside [0, n_slots), writes nothing, attends with q = 0 and puts 1 + its
+ * index into *error_word (may be NULL) -- as the two-launch form treats it. qkv as for
+ * mi_qk_norm_rope_write (T values, or fp32 split-K partials when qkv_parts >= 1), 16-byte
+ * aligned rows; the other arguments as for mi_paged_decode (strides' q entries are not
+ * read). Supported: head_dim 128, rotary_dim == 128, norm_mode 0 (Qwen3), fp16/bf16;
+ * anything else is MI_ERR_UNSUPPORTED (use the two entry points). */
+int mi_paged_decode_fused(const void* qkv, int64_t row_stride, int qkv_parts, const void* q_norm_w,
+                          const void* k_norm_w, const void* cos_tab, const void* sin_tab, int64_t n_pos,
+                          int rotary_dim, const int64_t* pos, const void* slot_ids, int slot_bits,
+                          void* k_cache, void* v_cache, const int32_t* block_table, const int32_t* seqlen,
+                          void* out, int B, int H, int H_kv, int D, int block_size, int max_blocks,
+                          int64_t n_slots, const int64_t* strides, float scale, float eps, int norm_mode,
+                          int dtype, void* workspace, size_t workspace_bytes, int32_t* error_word,
+                          void* stream);
+
 /* mi_paged_decode_noalloc -- no counterpart in the reference: for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc). mi_paged_decode with the same arguments minus the workspace: the

@@ -39,4 +39,4 @@ int launch_status(const char* what) {
 
 extern "C" const char* mi_last_error(void) { return miattn::g_last_error; }
 
-extern "C" int mi_abi_version(void) { return 12; }
+extern "C" int mi_abi_version(void) { return 13; }

@@ -128,6 +128,8 @@ constexpr int kDppQuadXor1 = 0xB1;
 constexpr int kDppQuadXor2 = 0x4E;
 constexpr int kDppRowHalfMirror = 0x141;
 constexpr int kDppRowMirror = 0x140;
+// row_ror:8: lane i of each 16-lane row reads lane (i + 8) mod 16 (the other half-row).
+constexpr int kDppRowRor8 = 0x128;
 
 // Exchange with lane ^ 16 (inside each 32-lane half) via ds_swizzle bitmask mode.
 __device__ __forceinline__ float swap16(float x) {
@@ -168,6 +170,17 @@ __device__ __forceinline__ float group_allreduce(float x) {
   if constexpr (W >= 32) x = Op::op(x, swap16(x));
   if constexpr (W >= 64) x = Op::op(x, swap32(x));
   return x;
+}
+
+// Round an fp32 result to T (the rounding a tensor op of dtype T applies to its result).
+// The value goes through an empty asm first: without it the compiler may fold
+// round_T(op_f32(a, b)) into the native fp16 op (division, square root), whose rounding
+// differs from the fp32 op rounded once (measured: 21% of fp16 outputs one ulp off the
+// tensor ops).
+template <typename T>
+__device__ __forceinline__ float rt(float x) {
+  asm volatile("" : "+v"(x));
+  return to_f32(from_f32<T>(x));
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

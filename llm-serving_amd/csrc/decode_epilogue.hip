@@ -40,16 +40,6 @@
 namespace miattn {
 namespace {
 
-// Round an fp32 result to T. The value goes through an empty asm first: without it the
-// compiler may fold round_T(op_f32(a, b)) into the native fp16 op (division, square root),
-// whose rounding differs from the fp32 op rounded once (measured: 21% of fp16 outputs one
-// ulp off the tensor ops).
-template <typename T>
-__device__ __forceinline__ float rt(float x) {
-  asm volatile("" : "+v"(x));
-  return to_f32(from_f32<T>(x));
-}
-
 // Which q/k norm the epilogue applies (see the file comment).
 enum NormMode { kNormQwen3 = 0, kNormZeroCentred = 1 };
 

@@ -49,6 +49,27 @@ struct DecodeArgs {
   float scale_log2;
 };
 
+// Inputs of the fused form (mi_paged_decode_fused): each row's packed q/k/v projection
+// ([q (H x D) | k (H_kv x D) | v (H_kv x D)] with row stride row_stride, as T values or as
+// fp32 split-K partials [parts][B][row_stride]), the q/k RMSNorm weights, the RoPE tables
+// (n_pos x D/2), each row's position and write slot.
+struct FusedArgs {
+  const void* qkv;
+  int64_t row_stride, plane;
+  int parts, slot_bits;
+  const void* q_w;
+  const void* k_w;
+  const void* cos_tab;
+  const void* sin_tab;
+  int64_t n_pos, n_slots;
+  const int64_t* pos;
+  const void* slots;
+  void* k_pool;  // the layer's pools (the kernel's k/v inputs), written at the new token's slot
+  void* v_pool;
+  float eps;
+  int32_t* err;
+};
+
 #ifndef MIATTN_DECODE_THREADS
 #define MIATTN_DECODE_THREADS 256
 #endif
@@ -224,12 +245,12 @@ __device__ __forceinline__ bool plan_split(const int32_t* __restrict__ seqlen, i
 // entries are wave-uniform and read with scalar loads. Those are counted apart from the
 // K/V vector loads, so the in-order vector-load counter tracks only K/V batches and the
 // reduction of batch i never waits for batch i+1.
-template <typename T, int D, int GB, bool UP>
+template <typename T, int D, int GB, bool UP, bool kFused>
 __global__ __launch_bounds__(kThreads) void paged_decode_kernel(
     const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc,
     const int32_t* __restrict__ block_table, const int32_t* __restrict__ seqlen,
     T* __restrict__ out, int32_t* __restrict__ ws_rows, float* __restrict__ ws_ml,
-    float* __restrict__ ws_acc, DecodeArgs a) {
+    float* __restrict__ ws_acc, DecodeArgs a, FusedArgs f) {
   using Lay = Layout<T, D, GB>;
   constexpr int EPL = Lay::EPL, LPR = Lay::LPR, RPW = Lay::RPW, NR = Lay::NR, U = Lay::U;
   extern __shared__ float smem[];  // parked row states: [TPL-1][KVB][GB] (m, l), then acc
@@ -329,8 +350,146 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(
   };
 
   uint4 qr[GB];
+  // Fused form: the row's new token (position len - 1, the last of the last split) has its
+  // k and v computed here and kept in registers; the split's masked final batch reads them
+  // instead of the pool, which this workgroup writes them to (no other workgroup reads
+  // that token, so nothing waits for the write).
+  int t_new = -1;
+  uint4 k_new = make_uint4(0u, 0u, 0u, 0u), v_new = make_uint4(0u, 0u, 0u, 0u);
+  // fused form, first half: every input load, none of them waiting on another (the row's
+  // position and slot, its projection columns, the norm weights); the second half, after
+  // the first K/V batches are issued, loads the RoPE rows at the position and computes.
+  constexpr int kNX = GB + 2;  // q heads, then this lane's KV head's k and v
+  float4 raw[kNX][2][2];       // [input][partial 0 / 1][elements 0-3 / 4-7]
+  int64_t f_pb = 0, f_sl = -1;
+  uint4 wq = make_uint4(0u, 0u, 0u, 0u), wk = wq, cv = wq, sv = wq;
+  const bool last_split = t_end == len;
+  auto col_of = [&](int ix) {
+    return ix < GB ? (h0 + ix) * D : ix == GB ? (a.H + kvh) * D : (a.H + a.H_kv + kvh) * D;
+  };
+  if constexpr (!kFused) {
 #pragma unroll
-  for (int g = 0; g < GB; ++g) qr[g] = load16(q + b * a.qs0 + (h0 + g) * a.qs1 + c * EPL);
+    for (int g = 0; g < GB; ++g) qr[g] = load16(q + b * a.qs0 + (h0 + g) * a.qs1 + c * EPL);
+  } else {
+    static_assert(D == 128 && EPL == 8 && LPR == 16, "fused form: head_dim 128, 16-bit types");
+    f_pb = f.pos[b];
+    f_sl = f.slot_bits == 32 ? int64_t(static_cast<const int32_t*>(f.slots)[b]) : static_cast<const int64_t*>(f.slots)[b];
+    const int ps = f.parts > 0 ? f.parts : 1;
+#pragma unroll
+    for (int ix = 0; ix < kNX; ++ix) {
+      if (ix >= GB && !last_split) break;
+      const int64_t off = b * f.row_stride + col_of(ix) + c * EPL;
+      if (f.parts == 0) {
+        const uint4 w = load16(static_cast<const T*>(f.qkv) + off);
+        raw[ix][0][0] = make_float4(__uint_as_float(w.x), __uint_as_float(w.y), __uint_as_float(w.z),
+                                    __uint_as_float(w.w));
+      } else {
+#pragma unroll
+        for (int pp = 0; pp < 2; ++pp) {
+          const float* fp = static_cast<const float*>(f.qkv) + int64_t(pp < ps ? pp : ps - 1) * f.plane + off;
+          raw[ix][pp][0] = *reinterpret_cast<const float4*>(fp);
+          raw[ix][pp][1] = *reinterpret_cast<const float4*>(fp + 4);
+        }
+      }
+    }
+    wq = load16(static_cast<const T*>(f.q_w) + c * EPL);
+    wk = load16(static_cast<const T*>(f.k_w) + c * EPL);
+    // the RoPE rows at the position the contract gives (len - 1), loaded without waiting for
+    // pos[b]; a row whose pos differs is refused below and never uses them
+    int64_t prow = int64_t(len) - 1;
+    prow = prow < f.n_pos ? prow : f.n_pos - 1;
+    prow = prow > 0 ? prow : 0;
+    cv = load16(static_cast<const T*>(f.cos_tab) + prow * (D / 2) + (c & 7) * EPL);
+    sv = load16(static_cast<const T*>(f.sin_tab) + prow * (D / 2) + (c & 7) * EPL);
+  }
+  // fused form, second half. q/k RMSNorm + RoPE, op by op as mi_qk_norm_rope_write
+  // computes them, in this kernel's lane layout: a head row is one 16-lane DPP row, lane c
+  // holding elements 8c .. 8c + 7. The sum of squares reproduces that kernel's 64-lane
+  // butterfly exactly: its lane l holds rt(x_l^2) + rt(x_{l+64}^2), here the pair (lane c,
+  // lane c + 8) forms those eight sums for l = 8(c mod 8) + j, the butterfly's levels 1-3
+  // (l ^ 1, ^ 2, ^ 4) are the in-lane tree over j and its levels 4-6 (l ^ 8, ^ 16, ^ 32) the
+  // 8-lane butterfly over c. The RoPE partner of element e (e +- 64) is lane c ^ 8's element j.
+  auto fused_finish = [&]() {
+    if constexpr (kFused) {
+      const bool idle = f_sl == -1;
+      const bool ok = !idle && f_pb >= 0 && f_pb < f.n_pos && f_sl >= 0 && f_sl < f.n_slots && f_pb == int64_t(len) - 1;
+      if (!idle && !ok && split == 0 && blockIdx.y == 0 && tid == 0 && f.err != nullptr) atomicCAS(f.err, 0, b + 1);
+      // input ix as T values (split-K partials summed in split order, rounded once)
+      auto values = [&](int ix, float (&x)[EPL]) {
+        if (f.parts == 0) {
+          const uint4 w = make_uint4(__float_as_uint(raw[ix][0][0].x), __float_as_uint(raw[ix][0][0].y),
+                                     __float_as_uint(raw[ix][0][0].z), __float_as_uint(raw[ix][0][0].w));
+  #pragma unroll
+          for (int j = 0; j < EPL; ++j) x[j] = Vec16<T>::get(w, j);
+        } else {
+          float s8[EPL] = {raw[ix][0][0].x, raw[ix][0][0].y, raw[ix][0][0].z, raw[ix][0][0].w,
+                           raw[ix][0][1].x, raw[ix][0][1].y, raw[ix][0][1].z, raw[ix][0][1].w};
+          if (f.parts > 1) {
+            const float p1[EPL] = {raw[ix][1][0].x, raw[ix][1][0].y, raw[ix][1][0].z, raw[ix][1][0].w,
+                                   raw[ix][1][1].x, raw[ix][1][1].y, raw[ix][1][1].z, raw[ix][1][1].w};
+  #pragma unroll
+            for (int j = 0; j < EPL; ++j) s8[j] += p1[j];
+          }
+          for (int pp = 2; pp < f.parts; ++pp) {
+            const float* fp = static_cast<const float*>(f.qkv) + int64_t(pp) * f.plane + b * f.row_stride + col_of(ix) +
+                              c * EPL;
+  #pragma unroll
+            for (int j = 0; j < EPL; ++j) s8[j] += fp[j];
+          }
+  #pragma unroll
+          for (int j = 0; j < EPL; ++j) x[j] = rt<T>(s8[j]);
+        }
+      };
+      auto norm_rope = [&](float (&x)[EPL], const uint4& w) {
+        float v8[EPL];
+  #pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+          const float sq = rt<T>(x[j] * x[j]);
+          v8[j] = sq + dpp<kDppRowRor8>(sq);
+        }
+        float ss = ((v8[0] + v8[1]) + (v8[2] + v8[3])) + ((v8[4] + v8[5]) + (v8[6] + v8[7]));
+        ss = group_allreduce<8, SumOp>(ss);
+        const float ms = rt<T>(ss * (1.0f / D));
+        const float rms = rt<T>(sqrtf(rt<T>(ms + f.eps)));
+        float y[EPL], o[EPL];
+  #pragma unroll
+        for (int j = 0; j < EPL; ++j) y[j] = rt<T>(rt<T>(x[j] / rms) * Vec16<T>::get(w, j));
+  #pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+          const float partner = dpp<kDppRowRor8>(y[j]);
+          const float cs = Vec16<T>::get(cv, j), sn = Vec16<T>::get(sv, j);
+          o[j] = c < 8 ? rt<T>(rt<T>(y[j] * cs) - rt<T>(partner * sn)) : rt<T>(rt<T>(partner * sn) + rt<T>(y[j] * cs));
+        }
+        return pack16<T>(o);
+      };
+      if (ok) {
+  #pragma unroll
+        for (int g = 0; g < GB; ++g) {
+          float x[EPL];
+          values(g, x);
+          qr[g] = norm_rope(x, wq);
+        }
+      } else {
+        // a row whose epilogue inputs are refused attends with q = 0, as the two-launch form
+        // (mi_qk_norm_rope_write leaves zeros in q_out) does
+  #pragma unroll
+        for (int g = 0; g < GB; ++g) qr[g] = make_uint4(0u, 0u, 0u, 0u);
+      }
+      if (ok && last_split) {
+        float xk[EPL], xv[EPL];
+        values(GB, xk);
+        values(GB + 1, xv);
+        k_new = norm_rope(xk, wk);
+        v_new = pack16<T>(xv);
+        t_new = len - 1;
+        if (tsub == t_new % TPL && hch == 0) {
+          const int64_t blk = f_sl >> a.bs_log2, in_blk = f_sl & ((1 << a.bs_log2) - 1);
+          store16(static_cast<T*>(f.k_pool) + blk * a.ks0 + in_blk * a.ks1 + kvh * a.ks2 + c * EPL, k_new);
+          store16(static_cast<T*>(f.v_pool) + blk * a.vs0 + in_blk * a.vs1 + kvh * a.vs2 + c * EPL, v_new);
+        }
+      }
+    }
+  };
 
   float m[GB], l[GB], acc[GB][EPL];
 #pragma unroll
@@ -350,7 +509,11 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(
     for (int u = 0; u < U; ++u) {
 #pragma unroll
       for (int g = 0; g < GB; ++g) {
-        float dot = dot16<T>(qr[g], kr[u], 0.0f);
+        uint4 kk = kr[u];
+        if constexpr (kFused && decltype(masked)::value) {
+          if (t0 + u * TPL + tsub == t_new) kk = k_new;
+        }
+        float dot = dot16<T>(qr[g], kk, 0.0f);
         dot = group_allreduce<LPR, SumOp>(dot);
         s[u][g] = dot * a.scale_log2;
         if constexpr (decltype(masked)::value) {
@@ -374,8 +537,12 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(
       for (int u = 0; u < U; ++u) {
         const float p = fast_exp2(s[u][g] - m_use);
         lsum_g += p;
+        uint4 vv = vr[u];
+        if constexpr (kFused && decltype(masked)::value) {
+          if (t0 + u * TPL + tsub == t_new) vv = v_new;
+        }
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) acc[g][e] = fmaf(p, Vec16<T>::get(vr[u], e), acc[g][e]);
+        for (int e = 0; e < EPL; ++e) acc[g][e] = fmaf(p, Vec16<T>::get(vv, e), acc[g][e]);
       }
       l[g] = lsum_g;
     }
@@ -407,6 +574,7 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(
   issue(t_begin, pgA, kA, vA);
   issue(t_begin + batch, pgB, kB, vB);  // unconditional (see above); n_b >= 1 always
   load_pages(t_begin + 2 * batch, pgA);
+  if constexpr (kFused) fused_finish();  // q (and the new token's k/v) while the batches land
   int i = 0;
   for (; i + 2 < n_b; i += 2) {
     const int t0 = t_begin + i * batch;
@@ -617,7 +785,7 @@ Plan make_plan(int B, int H, int H_kv, int D, int block_size, int max_blocks, in
 template <typename T, int D, int GB>
 int launch_typed(const void* q, const void* kc, const void* vc, const int32_t* bt,
                  const int32_t* seqlen, void* out, int32_t* ws_rows, float* ws_ml,
-                 float* ws_acc, const DecodeArgs& a, const Plan& p, hipStream_t stream) {
+                 float* ws_acc, const DecodeArgs& a, const Plan& p, const FusedArgs* fa, hipStream_t stream) {
   if (Layout<T, D, GB>::U != p.U || Layout<T, D, GB>::NR != p.NR) {
     return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode: internal launch-geometry mismatch");
   }
@@ -625,16 +793,24 @@ int launch_typed(const void* q, const void* kc, const void* vc, const int32_t* b
   // Wave-uniform pages need every wave inside one token (RPW <= KVB) and the lane byte
   // offsets within 32 bits.
   const int64_t lane_span = (int64_t(a.H_kv) * std::max(a.ks2, a.vs2) + D) * int64_t(sizeof(T));
-  if (Layout<T, D, GB>::RPW <= p.KVB && a.ks2 >= 0 && a.vs2 >= 0 && lane_span < (int64_t(1) << 31)) {
-    hipLaunchKernelGGL((paged_decode_kernel<T, D, GB, true>), grid, dim3(kThreads), p.smem_bytes,
-                       stream, static_cast<const T*>(q), static_cast<const T*>(kc),
-                       static_cast<const T*>(vc), bt, seqlen, static_cast<T*>(out), ws_rows, ws_ml,
-                       ws_acc, a);
+  const bool up = Layout<T, D, GB>::RPW <= p.KVB && a.ks2 >= 0 && a.vs2 >= 0 && lane_span < (int64_t(1) << 31);
+  auto go = [&](auto up_c, auto fused_c) {
+    hipLaunchKernelGGL((paged_decode_kernel<T, D, GB, decltype(up_c)::value, decltype(fused_c)::value>), grid,
+                       dim3(kThreads), p.smem_bytes, stream, static_cast<const T*>(q), static_cast<const T*>(kc),
+                       static_cast<const T*>(vc), bt, seqlen, static_cast<T*>(out), ws_rows, ws_ml, ws_acc, a,
+                       fa != nullptr ? *fa : FusedArgs{});
+  };
+  using Yes = std::true_type;
+  using No = std::false_type;
+  if (fa != nullptr) {
+    // the fused form exists for head_dim 128 in 16-bit types (the callers check)
+    if constexpr (D == 128 && sizeof(T) == 2) {
+      if (up) go(Yes{}, Yes{}); else go(No{}, Yes{});
+    } else {
+      return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode_fused: no fused kernel for head_dim %d", D);
+    }
   } else {
-    hipLaunchKernelGGL((paged_decode_kernel<T, D, GB, false>), grid, dim3(kThreads), p.smem_bytes,
-                       stream, static_cast<const T*>(q), static_cast<const T*>(kc),
-                       static_cast<const T*>(vc), bt, seqlen, static_cast<T*>(out), ws_rows, ws_ml,
-                       ws_acc, a);
+    if (up) go(Yes{}, No{}); else go(No{}, No{});
   }
   int rc = launch_status("mi_paged_decode (split kernel)");
   if (rc != MI_OK) return rc;
@@ -647,12 +823,12 @@ int launch_typed(const void* q, const void* kc, const void* vc, const int32_t* b
 template <typename T, int D>
 int dispatch_gb(const void* q, const void* kc, const void* vc, const int32_t* bt,
                 const int32_t* seqlen, void* out, int32_t* ws_rows, float* ws_ml, float* ws_acc,
-                const DecodeArgs& a, const Plan& p, hipStream_t s) {
+                const DecodeArgs& a, const Plan& p, const FusedArgs* fa, hipStream_t s) {
   switch (p.GB) {
-    case 1: return launch_typed<T, D, 1>(q, kc, vc, bt, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, s);
-    case 2: return launch_typed<T, D, 2>(q, kc, vc, bt, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, s);
-    case 4: return launch_typed<T, D, 4>(q, kc, vc, bt, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, s);
-    case 8: return launch_typed<T, D, 8>(q, kc, vc, bt, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, s);
+    case 1: return launch_typed<T, D, 1>(q, kc, vc, bt, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, fa, s);
+    case 2: return launch_typed<T, D, 2>(q, kc, vc, bt, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, fa, s);
+    case 4: return launch_typed<T, D, 4>(q, kc, vc, bt, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, fa, s);
+    case 8: return launch_typed<T, D, 8>(q, kc, vc, bt, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, fa, s);
   }
   return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode: no kernel for %d heads per lane", p.GB);
 }
@@ -660,15 +836,15 @@ int dispatch_gb(const void* q, const void* kc, const void* vc, const int32_t* bt
 template <typename T>
 int dispatch_d(int D, const void* q, const void* kc, const void* vc, const int32_t* bt,
                const int32_t* seqlen, void* out, int32_t* ws_rows, float* ws_ml, float* ws_acc,
-               const DecodeArgs& a, const Plan& p, hipStream_t s) {
+               const DecodeArgs& a, const Plan& p, const FusedArgs* fa, hipStream_t s) {
   switch (D) {
     case 16:
-      if constexpr (sizeof(T) == 2) return dispatch_gb<T, 16>(q, kc, vc, bt, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, s);
+      if constexpr (sizeof(T) == 2) return dispatch_gb<T, 16>(q, kc, vc, bt, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, fa, s);
       break;
-    case 32: return dispatch_gb<T, 32>(q, kc, vc, bt, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, s);
-    case 64: return dispatch_gb<T, 64>(q, kc, vc, bt, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, s);
-    case 128: return dispatch_gb<T, 128>(q, kc, vc, bt, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, s);
-    case 256: return dispatch_gb<T, 256>(q, kc, vc, bt, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, s);
+    case 32: return dispatch_gb<T, 32>(q, kc, vc, bt, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, fa, s);
+    case 64: return dispatch_gb<T, 64>(q, kc, vc, bt, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, fa, s);
+    case 128: return dispatch_gb<T, 128>(q, kc, vc, bt, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, fa, s);
+    case 256: return dispatch_gb<T, 256>(q, kc, vc, bt, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, fa, s);
   }
   return fail(MI_ERR_UNSUPPORTED,
               "mi_paged_decode: head_dim %d is not supported by the HIP decode kernel "
@@ -700,7 +876,7 @@ namespace {
 int paged_decode_entry(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
                        const int32_t* seqlen, void* out, int B, int H, int H_kv, int D, int block_size,
                        int max_blocks, const int64_t* strides, float scale, int dtype, void* workspace,
-                       size_t workspace_bytes, void* stream) {
+                       size_t workspace_bytes, void* stream, FusedArgs* fa = nullptr) {
   if (esize_of(dtype) == 0) return fail(MI_ERR_INVALID, "mi_paged_decode: unknown dtype %d", dtype);
   if (B < 0 || H < 1 || H_kv < 1 || H % H_kv != 0) {
     return fail(MI_ERR_INVALID, "mi_paged_decode: n_head (%d) must be a multiple of n_kv_head (%d)",
@@ -769,10 +945,14 @@ int paged_decode_entry(const void* q, const void* k_cache, const void* v_cache, 
   a.scale_log2 = scale * 1.4426950408889634f;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (fa != nullptr) {
+    fa->k_pool = const_cast<void*>(k_cache);
+    fa->v_pool = const_cast<void*>(v_cache);
+  }
   switch (dtype) {
-    case MI_F32: return dispatch_d<float>(D, q, k_cache, v_cache, block_table, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, s);
-    case MI_F16: return dispatch_d<f16_t>(D, q, k_cache, v_cache, block_table, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, s);
-    case MI_BF16: return dispatch_d<bf16_t>(D, q, k_cache, v_cache, block_table, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, s);
+    case MI_F32: return dispatch_d<float>(D, q, k_cache, v_cache, block_table, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, fa, s);
+    case MI_F16: return dispatch_d<f16_t>(D, q, k_cache, v_cache, block_table, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, fa, s);
+    case MI_BF16: return dispatch_d<bf16_t>(D, q, k_cache, v_cache, block_table, seqlen, out, ws_rows, ws_ml, ws_acc, a, p, fa, s);
   }
   return fail(MI_ERR_INVALID, "mi_paged_decode: unknown dtype %d", dtype);
 }
@@ -826,6 +1006,68 @@ extern "C" int mi_paged_decode(const void* q, const void* k_cache, const void* v
                                size_t workspace_bytes, void* stream) {
   return miattn::paged_decode_entry(q, k_cache, v_cache, block_table, seqlen, out, B, H, H_kv, D, block_size,
                                     max_blocks, strides, scale, dtype, workspace, workspace_bytes, stream);
+}
+
+extern "C" int mi_paged_decode_fused(const void* qkv, int64_t row_stride, int qkv_parts, const void* q_norm_w,
+                                     const void* k_norm_w, const void* cos_tab, const void* sin_tab, int64_t n_pos,
+                                     int rotary_dim, const int64_t* pos, const void* slot_ids, int slot_bits,
+                                     void* k_cache, void* v_cache, const int32_t* block_table, const int32_t* seqlen,
+                                     void* out, int B, int H, int H_kv, int D, int block_size, int max_blocks,
+                                     int64_t n_slots, const int64_t* strides, float scale, float eps, int norm_mode,
+                                     int dtype, void* workspace, size_t workspace_bytes, int32_t* error_word,
+                                     void* stream) {
+  using namespace miattn;
+  if (dtype != MI_BF16 && dtype != MI_F16) {
+    return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode_fused: fp16/bf16 only, got dtype %d", dtype);
+  }
+  if (D != 128 || rotary_dim != D || norm_mode != 0) {
+    return fail(MI_ERR_UNSUPPORTED,
+                "mi_paged_decode_fused: head_dim 128 with whole-head RoPE and the Qwen3 norm only (got head_dim "
+                "%d, rotary_dim %d, norm_mode %d); use mi_qk_norm_rope_write and mi_paged_decode",
+                D, rotary_dim, norm_mode);
+  }
+  if (B < 0 || H < 1 || H_kv < 1 || H % H_kv != 0) {
+    return fail(MI_ERR_INVALID, "mi_paged_decode_fused: n_head (%d) must be a multiple of n_kv_head (%d)", H, H_kv);
+  }
+  if (slot_bits != 32 && slot_bits != 64) {
+    return fail(MI_ERR_INVALID, "mi_paged_decode_fused: slot_bits must be 32 or 64, got %d", slot_bits);
+  }
+  if (n_pos < 1 || n_slots < 1 || qkv_parts < 0) {
+    return fail(MI_ERR_INVALID, "mi_paged_decode_fused: n_pos %lld, n_slots %lld, qkv_parts %d",
+                (long long)n_pos, (long long)n_slots, qkv_parts);
+  }
+  if (row_stride < int64_t(H + 2 * H_kv) * D) {
+    return fail(MI_ERR_INVALID, "mi_paged_decode_fused: row stride %lld < %d packed q/k/v elements",
+                (long long)row_stride, (H + 2 * H_kv) * D);
+  }
+  if (qkv == nullptr || q_norm_w == nullptr || k_norm_w == nullptr || cos_tab == nullptr || sin_tab == nullptr ||
+      pos == nullptr || slot_ids == nullptr) {
+    return fail(MI_ERR_INVALID, "mi_paged_decode_fused: a required pointer is NULL");
+  }
+  const int64_t in_es = qkv_parts > 0 ? 4 : 2;
+  auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  if (!al(qkv) || (row_stride * in_es) % 16 != 0 || !al(q_norm_w) || !al(k_norm_w) || !al(cos_tab) || !al(sin_tab)) {
+    return fail(MI_ERR_UNSUPPORTED,
+                "mi_paged_decode_fused: qkv rows, norm weights and RoPE tables must be 16-byte aligned");
+  }
+  FusedArgs fa{};
+  fa.qkv = qkv;
+  fa.row_stride = row_stride;
+  fa.plane = int64_t(B) * row_stride;
+  fa.parts = qkv_parts;
+  fa.slot_bits = slot_bits;
+  fa.q_w = q_norm_w;
+  fa.k_w = k_norm_w;
+  fa.cos_tab = cos_tab;
+  fa.sin_tab = sin_tab;
+  fa.n_pos = n_pos;
+  fa.n_slots = n_slots;
+  fa.pos = pos;
+  fa.slots = slot_ids;
+  fa.eps = eps;
+  fa.err = error_word;
+  return paged_decode_entry(nullptr, k_cache, v_cache, block_table, seqlen, out, B, H, H_kv, D, block_size,
+                            max_blocks, strides, scale, dtype, workspace, workspace_bytes, stream, &fa);
 }
 
 // The split-K partials need no clearing between calls: a row's (first slot, split count)

@@ -65,6 +65,13 @@ SIGNATURES: dict[str, tuple] = {
          _c_int, _c_int, _c_int, _c_int, _p_int64, _c_float, _c_int, _c_void_p, _c_size_t,
          _c_void_p],
     ),
+    "mi_paged_decode_fused": (
+        _c_int,
+        [_c_void_p, _c_int64, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int64, _c_int, _c_void_p,
+         _c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
+         _c_int, _c_int, _c_int, _c_int64, _p_int64, _c_float, _c_float, _c_int, _c_int, _c_void_p, _c_size_t,
+         _c_void_p, _c_void_p],
+    ),
     "mi_paged_decode_noalloc": (
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int,
@@ -127,7 +134,7 @@ SIGNATURES: dict[str, tuple] = {
     "mi_prefill_wait_limit": (_c_int, [_c_int]),
 }
 
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 
 def _load():

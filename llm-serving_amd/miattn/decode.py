@@ -311,6 +311,62 @@ class PagedDecodePlan:
         return out
 
 
+    def fused_supported(self, dtype: torch.dtype, rotary_dim: int, zero_centred_norm: bool = False) -> bool:
+        """Whether :meth:`run_fused` covers this geometry: head_dim 128, whole-head RoPE, the
+        Qwen3 q/k norm, fp16/bf16 (``mi_paged_decode_fused``)."""
+        return (self.geometry.head_dim == 128 and int(rotary_dim) == 128 and not zero_centred_norm
+                and dtype in (torch.float16, torch.bfloat16))
+
+    def run_fused(self, layer: int, qkv, q_norm_w, k_norm_w, cos, sin, pos, slot_ids, eps: float, *,
+                  error_word: torch.Tensor | None = None) -> torch.Tensor:
+        """One layer's decode attention straight from its packed q/k/v projection: q/k RMSNorm,
+        RoPE at ``pos`` and the new token's K/V write into this layer's pools, then the paged
+        decode -- ``PagedPool.write_qk_norm_rope`` followed by :meth:`run`, with the same
+        result bit for bit, in one launch pair (``mi_paged_decode_fused``). ``qkv`` is the
+        ``(B, (H + 2 H_kv) D)`` projection or its split-K partial sums (an object with
+        ``data`` ``(S, B, width)`` fp32 and ``n_parts``); ``pos`` int64 ``(B,)`` must be each
+        row's last position (``seqlen - 1``); ``slot_ids`` int32/int64 ``(B,)``, -1 for an idle
+        row. Rows refused for a position or slot out of range are reported through
+        ``error_word`` (1 + row) and attend with q = 0. Returns ``(B, H, D)``."""
+        if not 0 <= int(layer) < self.n_layer:
+            raise IndexError(f"layer {layer} is outside the plan's {self.n_layer} layers")
+        g = self.geometry
+        dtype = self.q_signature[1]
+        width = (g.q_heads + 2 * g.kv_heads) * g.head_dim
+        if hasattr(qkv, "n_parts"):
+            source, n_parts = qkv.data, int(qkv.n_parts)
+            if tuple(source.shape[1:]) != (g.rows, width) or source.dtype != torch.float32:
+                raise ValueError(f"qkv partials must be (S, {g.rows}, {width}) fp32, got {tuple(source.shape)}")
+            row_stride = width
+        else:
+            source, n_parts = qkv, 0
+            if qkv.dim() != 2 or tuple(qkv.shape) != (g.rows, width) or qkv.stride(1) != 1 or qkv.dtype != dtype:
+                raise ValueError(f"qkv must be ({g.rows}, {width}) {dtype} with unit element stride, got "
+                                 f"{qkv.dtype} {tuple(qkv.shape)}")
+            row_stride = qkv.stride(0)
+        rotary = 2 * int(cos.shape[-1])
+        if not self.fused_supported(dtype, rotary):
+            raise ValueError("run_fused covers head_dim 128 with whole-head RoPE in fp16/bf16; use "
+                             "PagedPool.write_qk_norm_rope and run")
+        if cos.shape != sin.shape or cos.dim() != 2 or not (cos.is_contiguous() and sin.is_contiguous()):
+            raise ValueError(f"cos/sin must be contiguous (n_pos, 64) tables, got {tuple(cos.shape)}")
+        if pos.dtype != torch.int64 or pos.numel() != g.rows or slot_ids.numel() != g.rows or \
+                slot_ids.dtype not in (torch.int32, torch.int64):
+            raise ValueError("pos must be int64 (B,) and slot_ids int32/int64 (B,)")
+        out = torch.empty(self.q_signature[0], dtype=dtype, device=self.q_signature[2])
+        k, v = self._pools[0][layer], self._pools[1][layer]
+        rc = _lib.lib.mi_paged_decode_fused(
+            source.data_ptr(), row_stride, n_parts, q_norm_w.data_ptr(), k_norm_w.data_ptr(), cos.data_ptr(),
+            sin.data_ptr(), int(cos.shape[0]), rotary, pos.data_ptr(), slot_ids.data_ptr(),
+            8 * slot_ids.element_size(), k.data_ptr(), v.data_ptr(), self._table.data_ptr(), self._seqlen.data_ptr(),
+            out.data_ptr(), *g.dims(), int(k.shape[0]) * int(k.shape[1]), self._strides, self._scale, float(eps), 0,
+            _lib.dtype_code(dtype), None if self._ws is None else self._ws.data_ptr(), self._ws_bytes,
+            None if error_word is None else error_word.data_ptr(), _lib.current_stream(out.device),
+        )
+        _lib.check(rc, "paged_decode_plan.run_fused")
+        return out
+
+
 def paged_decode_plan(q, k_caches, v_caches, block_table, seqlen, *, scale=None) -> PagedDecodePlan:
     """Check one container's decode tensors once and freeze their launch arguments
     (reference ``model/triton_decode.py:523-538``)."""

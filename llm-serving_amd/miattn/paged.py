@@ -256,6 +256,13 @@ class PagedPool:
             self.check_writes()
         return q
 
+    @property
+    def write_error_word(self) -> torch.Tensor | None:
+        """The device word a HIP write reports a refused token through (1 + its index; the
+        first report wins until :meth:`check_writes` reads and clears it); None for a host
+        pool."""
+        return self._write_error
+
     def check_writes(self) -> None:
         """Raise ``IndexError`` if a HIP write since the last check skipped a token whose
         slot (or position) was out of range; every in-range token was written. One host

@@ -368,6 +368,8 @@ class GraphDecoder:
         q0 = torch.zeros(B, c.n_head, c.head_dim, dtype=model.dtype, device=dev)
         self.plan = paged_decode_plan(q0, pool.keys, pool.values, self.table, self.seqlen,
                                       scale=1.0 / math.sqrt(c.head_dim))
+        # q/k norm + RoPE + K/V write fused into the decode launch where the shape allows
+        self.fused = self.plan.fused_supported(model.dtype, 2 * int(model.cos.shape[-1]))
         self.graph = None
 
     def _step(self) -> None:
@@ -381,6 +383,9 @@ class GraphDecoder:
 
         def attend(i: int, qkv) -> torch.Tensor:
             p = f"l{i}."
+            if self.fused:
+                return self.plan.run_fused(i, qkv, m.w[p + "qn"], m.w[p + "kn"], m.cos, m.sin, self.pos, slots,
+                                           c.eps, error_word=self.pool.write_error_word).view(self.B, -1)
             q = self.pool.write_qk_norm_rope(i, slots, qkv, m.w[p + "qn"], m.w[p + "kn"], m.cos, m.sin,
                                              self.pos, c.eps)
             return self.plan.run(i, q).view(self.B, -1)
