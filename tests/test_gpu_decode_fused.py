@@ -22,10 +22,12 @@ from miattn.rows import Parts
 pytestmark = pytest.mark.gpu
 
 H, H_KV, D, BS, EPS = 16, 8, 128, 16, 1e-6
-WIDTH = (H + 2 * H_KV) * D
 
 
-def _case(lengths, *, parts, dtype=torch.bfloat16, seed=0, n_pos=4096, slot_bits=64, idle=(), bad_slot=()):
+def _case(lengths, *, parts, dtype=torch.bfloat16, seed=0, n_pos=4096, slot_bits=64, idle=(), bad_slot=(),
+          heads=(H, H_KV)):
+    n_head, n_kv = heads
+    width_qkv = (n_head + 2 * n_kv) * D
     g = torch.Generator().manual_seed(seed)
     B = len(lengths)
     need = [max(1, -(-n // BS)) for n in lengths]
@@ -38,10 +40,10 @@ def _case(lengths, *, parts, dtype=torch.bfloat16, seed=0, n_pos=4096, slot_bits
         table[r, :k] = torch.tensor(perm[at:at + k], dtype=torch.int32)
         at += k
     pools = []
-    keys = torch.randn(n_blocks, BS, H_KV, D, generator=g).to(dtype)
-    vals = torch.randn(n_blocks, BS, H_KV, D, generator=g).to(dtype)
+    keys = torch.randn(n_blocks, BS, n_kv, D, generator=g).to(dtype)
+    vals = torch.randn(n_blocks, BS, n_kv, D, generator=g).to(dtype)
     for _ in range(2):
-        pool = PagedPool(1, n_blocks, BS, H_KV, D, dtype=dtype, device="cuda", n_head=H)
+        pool = PagedPool(1, n_blocks, BS, n_kv, D, dtype=dtype, device="cuda", n_head=n_head)
         pool.keys[0].copy_(keys)
         pool.values[0].copy_(vals)
         pools.append(pool)
@@ -54,9 +56,9 @@ def _case(lengths, *, parts, dtype=torch.bfloat16, seed=0, n_pos=4096, slot_bits
     for r in bad_slot:
         slots[r] = n_blocks * BS + 3
     if parts:
-        qkv = Parts((torch.randn(parts, B, WIDTH, generator=g) * 2.0).cuda(), dtype)
+        qkv = Parts((torch.randn(parts, B, width_qkv, generator=g) * 2.0).cuda(), dtype)
     else:
-        qkv = (torch.randn(B, WIDTH, generator=g) * 2.0).to(dtype).cuda()
+        qkv = (torch.randn(B, width_qkv, generator=g) * 2.0).to(dtype).cuda()
     qn = (1.0 + 0.1 * torch.randn(D, generator=g)).to(dtype).cuda()
     kn = (1.0 + 0.1 * torch.randn(D, generator=g)).to(dtype).cuda()
     cos, sin = rope_table(D, 1e6, n_pos, "cuda", dtype)
@@ -67,7 +69,7 @@ def _case(lengths, *, parts, dtype=torch.bfloat16, seed=0, n_pos=4096, slot_bits
 def _both(case):
     pools, table, seqlen, pos, slots, qkv, qn, kn, cos, sin = case
     B = table.shape[0]
-    q0 = torch.zeros(B, H, D, dtype=pools[0].dtype, device="cuda")
+    q0 = torch.zeros(B, pools[0].n_head, D, dtype=pools[0].dtype, device="cuda")
     plan_a = paged_decode_plan(q0, pools[0].keys, pools[0].values, table, seqlen)
     plan_b = paged_decode_plan(q0, pools[1].keys, pools[1].values, table, seqlen)
     q = pools[0].write_qk_norm_rope(0, slots, qkv, qn, kn, cos, sin, pos, EPS)
@@ -133,3 +135,12 @@ def test_fused_rejects_shapes_it_does_not_cover():
         plan.run_fused(0, qkv, qn, kn, cos[:, :32].contiguous(), sin[:, :32].contiguous(), pos, slots, EPS)
     with pytest.raises(ValueError, match="int64"):
         plan.run_fused(0, qkv, qn, kn, cos, sin, pos.int(), slots, EPS)
+
+
+@pytest.mark.parametrize("heads", [(16, 16), (32, 4), (8, 2), (64, 8)], ids=["mha16", "gqa8-4kv", "gqa4-2kv", "gqa8-8kv"])
+def test_fused_other_head_groupings(heads):
+    """Other GQA groupings at head_dim 128: the workgroup's KV heads and query heads per lane
+    change, and with them which q heads each lane normalises and rotates; bit-equal to the two
+    launches."""
+    pools, out_a, out_b = _both(_case([5, 700, 33, 1500, 129], parts=2, seed=13, heads=heads))
+    _assert_same(pools, out_a, out_b)
