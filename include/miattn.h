@@ -238,7 +238,12 @@ int mi_paged_decode(const void* q, const void* k_cache, const void* v_cache,
  * mi_qk_norm_rope_write (T values, or fp32 split-K partials when qkv_parts >= 1), 16-byte
  * aligned rows; the other arguments as for mi_paged_decode (strides' q entries are not
  * read). Supported: head_dim 128, rotary_dim == 128, norm_mode 0 (Qwen3), fp16/bf16;
- * anything else is MI_ERR_UNSUPPORTED (use the two entry points). */
+ * anything else is MI_ERR_UNSUPPORTED (use the two entry points). The new tokens' K/V are
+ * written while the launch reads the pools, so no row's slot may lie inside another row's
+ * first seqlen tokens (a block holding one row's new token mapped into another row's
+ * table below that row's length): such a row would read the old or the new value, where
+ * the two-launch form reads the new one. Tables of distinct blocks per row, as the
+ * reference's BlockManager hands out, never do. */
 int mi_paged_decode_fused(const void* qkv, int64_t row_stride, int qkv_parts, const void* q_norm_w,
                           const void* k_norm_w, const void* cos_tab, const void* sin_tab, int64_t n_pos,
                           int rotary_dim, const int64_t* pos, const void* slot_ids, int slot_bits,

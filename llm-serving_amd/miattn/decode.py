@@ -327,7 +327,10 @@ class PagedDecodePlan:
         ``data`` ``(S, B, width)`` fp32 and ``n_parts``); ``pos`` int64 ``(B,)`` must be each
         row's last position (``seqlen - 1``); ``slot_ids`` int32/int64 ``(B,)``, -1 for an idle
         row. Rows refused for a position or slot out of range are reported through
-        ``error_word`` (1 + row) and attend with q = 0. Returns ``(B, H, D)``."""
+        ``error_word`` (1 + row) and attend with q = 0. The new tokens' K/V are written while
+        the launch reads the pools, so no row's slot may fall inside another row's first
+        ``seqlen`` tokens (a block shared into another row's table below its length); the
+        reference's per-row blocks never do. Returns ``(B, H, D)``."""
         if not 0 <= int(layer) < self.n_layer:
             raise IndexError(f"layer {layer} is outside the plan's {self.n_layer} layers")
         g = self.geometry
