@@ -16,6 +16,8 @@
 // not two: 9.4 -> 8.7-9.0 us).
 // Sources with a non-unit element stride or 16-byte misalignment take the scalar kernel
 // (same bytes, element granularity).
+#include <type_traits>
+
 #include "common.h"
 
 namespace miattn {
@@ -31,20 +33,32 @@ __device__ __forceinline__ void record_bad_token(int32_t* err, int64_t token) {
 }
 
 // chunks_per_row = H_kv * D * esize / 16; chunks_per_head = D * esize / 16.
-// Source strides are in bytes here (the launcher converts).
-template <typename IdxT>
+// Source strides are in bytes here (the launcher converts). kPow2: both counts are powers of
+// two (row_log2 / head_log2 their logs), so a chunk's token, head and part come from shifts
+// and masks; otherwise from a 64-bit and a 32-bit division, ~130 instructions ahead of the
+// first load.
+template <typename IdxT, bool kPow2>
 __global__ __launch_bounds__(256) void slot_write_vec16(
     const uint8_t* __restrict__ k, const uint8_t* __restrict__ v, const IdxT* __restrict__ slots,
     uint8_t* __restrict__ k_pool, uint8_t* __restrict__ v_pool, int64_t n_tokens,
-    int chunks_per_row, int chunks_per_head, int64_t ks0, int64_t ks1, int64_t vs0, int64_t vs1,
-    int64_t n_slots, int32_t* err) {
+    int chunks_per_row, int chunks_per_head, int row_log2, int head_log2, int64_t ks0, int64_t ks1,
+    int64_t vs0, int64_t vs1, int64_t n_slots, int32_t* err) {
   const int64_t total = n_tokens * chunks_per_row;
   const int64_t stride = int64_t(gridDim.x) * blockDim.x;
   for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += stride) {
-    const int64_t token = i / chunks_per_row;
-    const int chunk = int(i - token * chunks_per_row);
-    const int head = chunk / chunks_per_head;
-    const int part = chunk - head * chunks_per_head;
+    int64_t token;
+    int chunk, head, part;
+    if constexpr (kPow2) {
+      token = i >> row_log2;
+      chunk = int(i & (chunks_per_row - 1));
+      head = chunk >> head_log2;
+      part = chunk & (chunks_per_head - 1);
+    } else {
+      token = i / chunks_per_row;
+      chunk = int(i - token * chunks_per_row);
+      head = chunk / chunks_per_head;
+      part = chunk - head * chunks_per_head;
+    }
     // the source rows do not depend on the slot: their loads go out with the slot id's, so
     // the chain is one memory round trip, not two
     uint4 kv = load16_nt(k + token * ks0 + head * ks1 + part * 16);
@@ -111,14 +125,24 @@ int launch(const void* k, const void* v, const IdxT* slots, void* k_pool, void* 
       (st[3] * esize) % 16 == 0 && (st[4] * esize) % 16 == 0;
   if (aligned) {
     const int chunks_per_row = int(row_bytes / 16);
+    const int chunks_per_head = int(int64_t(D) * esize / 16);
     const int64_t total = n_tokens * chunks_per_row;
     const int64_t blocks = (total + 255) / 256;
     const unsigned grid = unsigned(blocks < (1 << 20) ? blocks : (1 << 20));
-    hipLaunchKernelGGL(slot_write_vec16<IdxT>, dim3(grid), dim3(256), 0, stream,
-                       static_cast<const uint8_t*>(k), static_cast<const uint8_t*>(v), slots,
-                       static_cast<uint8_t*>(k_pool), static_cast<uint8_t*>(v_pool), n_tokens,
-                       chunks_per_row, int(int64_t(D) * esize / 16), st[0] * esize, st[1] * esize,
-                       st[3] * esize, st[4] * esize, n_slots, err);
+    auto log2_of = [](int x) { return (x & (x - 1)) == 0 ? __builtin_ctz(unsigned(x)) : -1; };
+    const int row_log2 = log2_of(chunks_per_row), head_log2 = log2_of(chunks_per_head);
+    auto go = [&](auto pow2) {
+      hipLaunchKernelGGL((slot_write_vec16<IdxT, decltype(pow2)::value>), dim3(grid), dim3(256), 0, stream,
+                         static_cast<const uint8_t*>(k), static_cast<const uint8_t*>(v), slots,
+                         static_cast<uint8_t*>(k_pool), static_cast<uint8_t*>(v_pool), n_tokens, chunks_per_row,
+                         chunks_per_head, row_log2, head_log2, st[0] * esize, st[1] * esize, st[3] * esize,
+                         st[4] * esize, n_slots, err);
+    };
+    if (row_log2 >= 0 && head_log2 >= 0) {
+      go(std::true_type{});
+    } else {
+      go(std::false_type{});
+    }
     return launch_status("mi_kv_slot_write");
   }
   const int64_t total = n_tokens * H_kv * D;
