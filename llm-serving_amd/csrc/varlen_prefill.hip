@@ -1364,13 +1364,19 @@ __global__ __launch_bounds__(Duo<D>::THREADS, Duo<D>::PER_CU) void varlen_prefil
 #pragma unroll
       for (int e = 1; e < 16; ++e) mloc = fmaxf(mloc, sc[e]);
       const float m_tile = max_halves(mloc) * scale_log2;
-      const bool moved = __any(m_tile > m_i + 8.0f);
-      const float m_new = moved ? fmaxf(m_i, m_tile) : m_i;
+      // Each query row (lanes l and l ^ 32 hold the same one, and max_halves gave both the
+      // same m_tile) moves its own reference max; the wave-wide vote only decides whether
+      // the O rescale after the MFMAs runs, so the exponentials do not wait for a VALU ->
+      // SALU -> VALU round trip (1.3% at head_dim 128). A row that did not move gets alpha
+      // = 1 exactly, so its O is unchanged by the rescale.
+      const bool mv = m_tile > m_i + 8.0f;
+      const float m_new = mv ? m_tile : m_i;
       const float m_use = m_new == -INFINITY ? 0.0f : m_new;
       const float alpha = fast_exp2(m_i - m_use);
       m_i = m_new;
 #pragma unroll
       for (int e = 0; e < 16; ++e) sc[e] = fast_exp2(fmaf(sc[e], scale_log2, -m_use));
+      const bool moved = __any(mv);
       // The row sum is taken from the fp32 probabilities, before their rounding for the PV
       // MFMA, as flash attention does. Summing the rounded ones (8 dot2) instead lowered the
       // end-to-end greedy agreement with the CPU seat path (closed case 252 against 254 of
@@ -1948,11 +1954,13 @@ __global__ __launch_bounds__(Tall<D>::THREADS, Tall<D>::PER_CU) void varlen_pref
       }
       const float mloc = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
       const float m_tile = max_halves(mloc) * scale_log2;
-      const bool moved = __any(m_tile > m_i + 8.0f);
-      const float m_new = moved ? fmaxf(m_i, m_tile) : m_i;
+      // per query row, as in the duo kernel: the vote only gates the O rescale
+      const bool mv = m_tile > m_i + 8.0f;
+      const float m_new = mv ? m_tile : m_i;
       const float m_use = m_new == -INFINITY ? 0.0f : m_new;
       const float alpha = fast_exp2(m_i - m_use);
       m_i = m_new;
+      const bool moved = __any(mv);
       float ls = l_i * alpha;
       // phase B, group q (of NG): K operands of group q+1 read, group q's PG MFMAs, and its
       // share of the exponentials (EPG of them, part of P's k-step (q * EPG) / 8)
