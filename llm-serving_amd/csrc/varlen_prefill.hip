@@ -1381,9 +1381,20 @@ __global__ __launch_bounds__(Duo<D>::THREADS, Duo<D>::PER_CU) void varlen_prefil
       // MFMA, as flash attention does. Summing the rounded ones (8 dot2) instead lowered the
       // end-to-end greedy agreement with the CPU seat path (closed case 252 against 254 of
       // 260 steps exact, trace case 1142 against 1153 of 1168), all fp32 near-ties.
-      float lsum = l_i * alpha;
+      // At head_dim 256 the sum is a tree (four levels, not a chain of 16 dependent adds):
+      // 37.9 against 38.4 us. At head_dim 64/128 it stays a chain: there the tree is within
+      // noise and its other rounding moved the closed greedy gate (253 against 254 of 260
+      // steps exact, every miss an fp32 near-tie).
+      float lsum;
+      if constexpr (D == 256) {
+        const float q0 = (sc[0] + sc[1]) + (sc[2] + sc[3]), q1 = (sc[4] + sc[5]) + (sc[6] + sc[7]);
+        const float q2 = (sc[8] + sc[9]) + (sc[10] + sc[11]), q3 = (sc[12] + sc[13]) + (sc[14] + sc[15]);
+        lsum = fmaf(l_i, alpha, (q0 + q1) + (q2 + q3));
+      } else {
+        lsum = l_i * alpha;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) lsum += sc[e];
+        for (int e = 0; e < 16; ++e) lsum += sc[e];
+      }
       // P(t) packed here, in the block of this step's MFMAs, and pinned with the row sum:
       // left alone the compiler sinks the exponentials past the end of the step, beside the
       // PV MFMAs that read P, where nothing hides them (2-3% of the kernel), and keeps the
