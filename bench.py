@@ -505,6 +505,23 @@ def bench_block32(stream, steps: int = 50) -> dict:
             "frac_hbm_peak": res["gbs"] / HBM_PEAK_GBS}
 
 
+def bench_decode_config1(stream, steps: int = 50) -> dict:
+    """Config 1's shape on the GPU kernel (the CPU seat path's workload in `cpu_baseline`):
+    B=8 rows of 512 tokens (511 cached + 1), H16/8/D128 bf16, block size 16, 28 layers of
+    512-block pools with permuted tables; checked then timed like the headline leg. (The
+    config-1 inputs themselves, RoPE pre-applied, are checked against the seat path in
+    tests/test_gpu_decode.py.)"""
+    from miattn import workloads as W
+
+    inp = W.paged_decode_config(device="cuda", B=8, lengths=[512] * 8, n_blocks=512)
+    res = bench_decode(inp, steps, 5, stream)
+    res.pop("out0")
+    del inp
+    torch.cuda.empty_cache()
+    return {"workload": "config1 shape: B=8 x 512 tokens, H16/H_kv8/D128 bf16, block 16, 28 layers, HIP-graph replay",
+            **res, "frac_hbm_peak": res["gbs"] / HBM_PEAK_GBS}
+
+
 def bench_decode_qwen35(stream, steps: int = 50) -> dict:
     """Config 2's lengths at the Qwen3.5 attention shape (H 8 / H_kv 2 / head_dim 256,
     block size 16, 8192 blocks per layer, 28 layers): checked then timed like the
@@ -802,6 +819,9 @@ def main() -> int:
         log(f"head-major pools: {line['decode_head_major']['us_per_layer']:.2f} us/layer")
         line["decode_qwen35"] = bench_decode_qwen35(stream)
         log(f"decode (Qwen3.5 shape, D256): {line['decode_qwen35']['us_per_layer']:.2f} us/layer")
+        line["decode_config1"] = bench_decode_config1(stream)
+        log(f"decode (config 1 shape, B=8 x 512): {line['decode_config1']['us_per_layer']:.2f} us/layer, "
+            f"{line['decode_config1']['gbs']:.1f} GB/s")
         log("long-context decode (config 4)")
         line["long_context"] = bench_long_context(stream)
         log(f"config4: {line['long_context']['gbs']:.1f} GB/s")
